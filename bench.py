@@ -1,0 +1,252 @@
+#!/usr/bin/env python3
+"""Paged-decode benchmark on one MI355X.
+
+Workload (one "step"): the decode attention of a random-init Qwen3-0.6B layer
+stack -- 16 Q / 8 KV heads, head_dim 128, bf16, block 16 -- for 32 sequences
+with contexts U[128, 2048] over a 16384-block pool per layer. A step is 28
+independent layer calls, each one KV append of the 32 new rows plus paged
+decode attention over that layer's own cache (28 distinct 1.07 GB caches, so
+nothing is served from the 256 MB last-level cache). The step is captured in
+a hipGraph and replayed; inputs are resident in HBM before timing.
+
+Prints one JSON line: value = whole-step algorithmic HBM bytes / step time
+(GB/s), the roofline of the decode layer call and a CPU-oracle baseline.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+
+        counts = [p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"]
+        return max(counts) if counts else 1
+    except Exception:  # pragma: no cover - informational only
+        return 1
+
+
+def build_decode_state(torch, layers: int, layout: str):
+    from microinfer_amd.workloads import QWEN3_06B, make_decode_batch
+    from microinfer_amd.worker.kv_cache import KVCache
+
+    batch = make_decode_batch(num_seqs=32, ctx_lo=128, ctx_hi=2048, pool_blocks=16384,
+                              draw_pools=False, **QWEN3_06B)
+    dev = torch.device("cuda", 0)
+    dtype = torch.bfloat16
+    cache = KVCache(layers, 16384, 16, 8, 128, dtype=dtype, device=dev, layout=layout)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    for layer in range(layers):
+        cache.keys[layer].copy_(torch.randn(cache.keys[layer].shape, generator=gen, device=dev))
+        cache.values[layer].copy_(torch.randn(cache.values[layer].shape, generator=gen, device=dev))
+    query = torch.empty((layers, 32, 16, 128), dtype=dtype, device=dev)
+    query[0].copy_(torch.from_numpy(batch.query))
+    query[1:].copy_(torch.randn(query[1:].shape, generator=gen, device=dev))
+    new_k = torch.randn((layers, 32, 8, 128), generator=gen, device=dev).to(dtype)
+    new_v = torch.randn((layers, 32, 8, 128), generator=gen, device=dev).to(dtype)
+    return dict(
+        batch=batch,
+        cache=cache,
+        views=[cache.layer(i) for i in range(layers)],
+        query=query,
+        new_k=new_k,
+        new_v=new_v,
+        tables=torch.tensor(batch.block_tables, device=dev),
+        lens=torch.tensor(batch.context_lens, device=dev),
+        slots=torch.tensor(batch.slots, device=dev),
+    )
+
+
+def cpu_baseline(torch, state, samples: int = 5):
+    """Oracle (numpy restatement of the reference CPU path) on layer 0's call."""
+    from microinfer_amd.workloads import decode_bytes
+    from oracle import kv_append, paged_attention_reference
+
+    batch = state["batch"]
+    view = state["views"][0]
+    tables = batch.block_tables
+    contexts = [int(c) for c in batch.context_lens]
+    used = sorted({int(b) for r, c in enumerate(contexts) for b in tables[r, : (c + 15) // 16]})
+    remap = {b: i for i, b in enumerate(used)}
+    small_tables = np.full_like(tables, -1)
+    for r, c in enumerate(contexts):
+        for j in range((c + 15) // 16):
+            small_tables[r, j] = remap[int(tables[r, j])]
+    index = torch.tensor(used, dtype=torch.long, device=view.keys.device)
+    # bf16 caches widen exactly to f32; the oracle accumulates in f32 as the
+    # reference does for half inputs (layer/paged_attention.py:38-40).
+    host_k = view.keys.index_select(0, index).float().cpu().numpy()
+    host_v = view.values.index_select(0, index).float().cpu().numpy()
+    q = state["query"][0].float().cpu().numpy()
+    nk = state["new_k"][0].float().cpu().numpy()
+    nv = state["new_v"][0].float().cpu().numpy()
+    slots = np.array([small_tables[r, (c - 1) // 16] * 16 + (c - 1) % 16
+                      for r, c in enumerate(contexts)])
+    cu = list(range(len(contexts) + 1))
+    scale = 1 / math.sqrt(128)
+
+    def one_call():
+        kv_append(host_k, host_v, slots, nk, nv)
+        return paged_attention_reference(q, host_k, host_v, small_tables, contexts, cu, scale=scale)
+
+    one_call()  # warm-up
+    times = []
+    for _ in range(samples):
+        t0 = time.perf_counter()
+        one_call()
+        times.append(time.perf_counter() - t0)
+    per_call = statistics.median(times)
+    nbytes = decode_bytes(contexts, num_q_heads=16, num_kv_heads=8, head_dim=128, elem_bytes=2,
+                          block_size=16)
+    return {
+        "value": round(nbytes / per_call / 1e9, 3),
+        "unit": "GB/s",
+        "cores": blas_threads(),
+        "kind": "port",
+        "sample": (f"1 layer call (KV append of 32 rows + decode over {sum(contexts)} cached "
+                   f"tokens, 0.6B shape) x {samples} runs after 1 warm-up, median "
+                   f"{per_call * 1e3:.1f} ms; numpy/BLAS on {os.cpu_count()} host CPUs "
+                   f"({cpu_model()})"),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--layers", type=int, default=28)
+    parser.add_argument("--layout", default="head_major", choices=["head_major", "token_major"])
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the decode shards by request or KV head with no exchange; see DESIGN.md).",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from microinfer_amd.layer.hip_paged_attention import hip_paged_decode
+    from microinfer_amd.workloads import decode_bytes
+
+    log("allocating 28-layer caches")
+    state = build_decode_state(torch, args.layers, args.layout)
+    views, query, tables, lens, slots = (state[k] for k in ("views", "query", "tables", "lens", "slots"))
+    new_k, new_v = state["new_k"], state["new_v"]
+    scale = 1 / math.sqrt(128)
+    outputs = []
+
+    def step():
+        outputs.clear()
+        for layer, view in enumerate(views):
+            view.write_slots(slots, new_k[layer], new_v[layer])
+            outputs.append(hip_paged_decode(query[layer], view.keys, view.values, tables, lens,
+                                            scale=scale))
+
+    step()
+    torch.cuda.synchronize()
+    log("capturing the decode step in a hipGraph")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = start.elapsed_time(end) / args.steps
+
+    contexts = state["batch"].context_lens
+    layer_bytes = decode_bytes(contexts, num_q_heads=16, num_kv_heads=8, head_dim=128,
+                               elem_bytes=2, block_size=16)
+    step_bytes = layer_bytes * args.layers
+    gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+    layer_us = ms_per_step * 1e3 / args.layers
+    log(f"{ms_per_step:.3f} ms/step, {layer_us:.2f} us/layer call, {gbs:.1f} GB/s "
+        f"(wall {wall:.2f} s)")
+
+    result = {
+        "metric": "paged-decode HBM GB/s (% peak) + decode tok/s, random-init Qwen3-0.6B b64",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) Q/K/V, random non-overlapping block tables",
+        "config": {
+            "workload": ("paged decode + KV append, Qwen3-0.6B attention (16 Q / 8 KV heads, "
+                         "head_dim 128), bf16, block 16, pool 16384 blocks per layer, "
+                         "32 sequences, contexts U[128,2048] (seed 0), 28 independent layer "
+                         "caches, hipGraph replay"),
+            "layers": args.layers,
+            "sum_context_tokens": int(np.sum(contexts)),
+            "kv_layout": args.layout,
+            "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+            "decode_tok_s": None,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "decode layer call (append + paged decode + split merge)",
+            "bytes_per_launch": layer_bytes,
+            "us_per_launch": round(layer_us, 3),
+        },
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle on layer 0")
+        result["cpu_baseline"] = cpu_baseline(torch, state)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,180 @@
+/*
+ * mi_attn.h -- C ABI of the MI355X (gfx950) paged-KV attention library.
+ *
+ * libmi_attn.so exports plain C entry points: device pointers, element
+ * strides, sizes, a dtype code and a hipStream_t passed as void*. No torch or
+ * C++ types cross this boundary. Every entry point
+ *   - launches asynchronously on `stream` and never synchronises,
+ *   - never allocates or frees device memory (callers pass any workspace),
+ *   - issues no memset/memcpy nodes, so it is safe inside hipGraph capture,
+ *   - returns MI_OK (0) or a non-zero status; mi_last_error() then describes
+ *     the failure (thread-local, valid until the next call on that thread).
+ *
+ * Cache layout: a layer's K (or V) cache is addressed as logical
+ * [num_blocks, block_size, num_kv_heads, head_dim] through three element
+ * strides (block, token, head); head_dim is contiguous. Both the reference's
+ * contiguous [N, B, Hkv, D] layout and the head-major [N, Hkv, B, D] layout of
+ * microinfer_amd.worker.kv_cache.KVCache are accepted.
+ *
+ * Index tensors (block tables, context lengths, cu_seqlens, slots) are int32
+ * device arrays unless a parameter says otherwise. Block ids outside
+ * [0, num_blocks) and slots < 0 are never dereferenced: such table entries are
+ * masked out of attention and such slots are skipped by the append.
+ */
+#ifndef MI_ATTN_H_
+#define MI_ATTN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type codes. */
+enum {
+  MI_DTYPE_F32 = 0,
+  MI_DTYPE_F16 = 1,
+  MI_DTYPE_BF16 = 2,
+};
+
+/* Status codes. */
+enum {
+  MI_OK = 0,
+  MI_ERR_INVALID_ARGUMENT = 1, /* shapes, strides, alignment, dtype */
+  MI_ERR_UNSUPPORTED = 2,      /* valid request this build has no kernel for */
+  MI_ERR_WORKSPACE = 3,        /* workspace missing or too small */
+  MI_ERR_HIP = 4,              /* launch or runtime error reported by HIP */
+};
+
+/* Description of the last failure on the calling thread ("" after success). */
+const char* mi_last_error(void);
+
+/* ABI version of this library (major * 100 + minor). */
+int32_t mi_abi_version(void);
+
+/*
+ * KV append: for every token t and KV head h,
+ *   key_cache[blk, off, h, :] = keys[t, h, :]   (and the same for values)
+ * with (blk, off) = (slot / block_size, slot % block_size).
+ *
+ * Replaces store_kv / _store_kv_kernel (microinfer/worker/triton_kv_store.py:45-78)
+ * plus the per-step slot div/mod of AttentionMetadata.slot_indices
+ * (microinfer/layer/metadata.py:75-84), both called from
+ * LayerKVCache.write_fast (microinfer/worker/kv_cache.py:52-79).
+ *
+ * index0/index1: if index1 is NULL, index0 holds slots (slot < 0 = padding,
+ * skipped, as in write_checked kv_cache.py:42). Otherwise index0 holds block
+ * ids and index1 in-block offsets (write_fast's precomputed form).
+ * index_is_int64 selects int64 (1) or int32 (0) indices.
+ * Slots whose block lies outside [0, num_blocks) are skipped.
+ */
+int32_t mi_kv_append(const void* keys, int64_t key_token_stride, int64_t key_head_stride,
+                     const void* values, int64_t value_token_stride,
+                     int64_t value_head_stride, void* key_cache, void* value_cache,
+                     int64_t cache_block_stride, int64_t cache_token_stride,
+                     int64_t cache_head_stride, const void* index0, const void* index1,
+                     int32_t index_is_int64, int32_t num_tokens, int32_t num_kv_heads,
+                     int32_t head_dim, int32_t block_size, int32_t num_blocks,
+                     int32_t dtype, void* stream);
+
+/*
+ * Paged decode attention: one query row per sequence,
+ *   out[s, h, :] = softmax_k(scale * q[s, h, :] . K[s, k, h / G, :]) V[s, k, h / G, :]
+ * over the context_lens[s] cached tokens of sequence s, G = Hq / Hkv.
+ *
+ * Replaces triton_paged_decode + _paged_decode_kernel + _paged_decode_reduce_kernel
+ * (microinfer/layer/triton_paged_attention.py:352-457, :40-131, :236-257), called
+ * from paged_attention_meta (microinfer/layer/paged_attention.py:232-246).
+ *
+ * One work item = (sequence, KV head, context partition); all G query heads of
+ * the KV head share it, so each K/V row is read from HBM once. split_k = 0
+ * picks partitions on the device from context_lens (graph-replay safe);
+ * split_k > 0 forces at most split_k partitions per sequence. Sequences with
+ * more than one partition are merged by a second, reduce launch.
+ *
+ * workspace: float32 device buffer of at least
+ * mi_paged_decode_workspace_bytes(...) bytes (may be NULL when that is 0).
+ * Sequences with context_len 0 produce zeros.
+ */
+int64_t mi_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
+                                        int32_t num_kv_heads, int32_t head_dim,
+                                        int32_t split_k);
+
+/*
+ * Tuning of the adaptive partition plan (split_k = 0): aim for about
+ * target_items (work item, KV head) wavefronts per launch, each covering at
+ * least min_part_blocks cache blocks. Values <= 0 leave a knob unchanged.
+ * Process-wide; changes the size mi_paged_decode_workspace_bytes reports, so
+ * set it before sizing workspaces or capturing graphs. Defaults 2048 / 2.
+ */
+void mi_tune_decode(int32_t target_items, int32_t min_part_blocks);
+
+int32_t mi_paged_decode(const void* query, int64_t q_token_stride, int64_t q_head_stride,
+                        const void* key_cache, const void* value_cache,
+                        int64_t cache_block_stride, int64_t cache_token_stride,
+                        int64_t cache_head_stride, const int32_t* block_tables,
+                        int64_t block_table_stride, int32_t block_table_width,
+                        const int32_t* context_lens, void* out, int64_t out_token_stride,
+                        int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
+                        int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                        int32_t head_dim, int32_t block_size, int32_t num_blocks,
+                        int32_t split_k, float scale, int32_t dtype, void* stream);
+
+/*
+ * Paged varlen (prefill / mixed) attention with a bottom-right causal mask:
+ * request r owns query rows [cu_seqlens_q[r], cu_seqlens_q[r+1]) and context
+ * c_r = cu_seqlens_k[r+1] - cu_seqlens_k[r]; its query row i sits at position
+ * (c_r - q_len_r) + i and attends to cached positions 0..that position
+ * (microinfer/layer/paged_attention.py:57-62).
+ *
+ * Replaces triton_paged_prefill + _paged_prefill_kernel
+ * (microinfer/layer/triton_paged_attention.py:260-339, :134-233) and the
+ * reference-path fallback of paged_attention_meta (paged_attention.py:277-293).
+ * bf16/f16 with head_dim 128 run on the MFMA kernel; every other supported
+ * shape (including f32) runs on the vector kernel. max_seqlen_q bounds the
+ * query rows of any request (launch shape only).
+ *
+ * block_tables == NULL selects contiguous varlen K/V instead of a paged cache:
+ * key_cache/value_cache are [sum c_r, Hkv, D] arrays (token stride
+ * cache_token_stride, head stride cache_head_stride) and request r's keys are
+ * rows cu_seqlens_k[r] .. cu_seqlens_k[r+1]-1; num_blocks then gives the
+ * number of K/V rows (rows at or past it are never read). This serves the no-prefix
+ * prefill that the reference routes to FlashAttention varlen or an SDPA loop
+ * (microinfer/layer/cached_attention.py:17-55, :87-101).
+ */
+int32_t mi_paged_prefill(const void* query, int64_t q_token_stride, int64_t q_head_stride,
+                         const void* key_cache, const void* value_cache,
+                         int64_t cache_block_stride, int64_t cache_token_stride,
+                         int64_t cache_head_stride, const int32_t* cu_seqlens_q,
+                         const int32_t* cu_seqlens_k, const int32_t* block_tables,
+                         int64_t block_table_stride, int32_t block_table_width,
+                         void* out, int64_t out_token_stride, int64_t out_head_stride,
+                         int32_t num_tokens, int32_t num_requests, int32_t max_seqlen_q,
+                         int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                         int32_t block_size, int32_t num_blocks, float scale,
+                         int32_t dtype, void* stream);
+
+/*
+ * Block-table gather: copy each request's first c_r cache rows, in logical
+ * order, into contiguous [sum c_r, Hkv, D] key_out / value_out, where
+ * c_r = cu_seqlens_k[r+1] - cu_seqlens_k[r] and request r's rows start at
+ * cu_seqlens_k[r]. Bit-exact copy.
+ *
+ * Replaces _gather_paged_kv (microinfer/layer/paged_attention.py:76-101), used by
+ * _paged_prefill_gather (:142-185) for the long-prompt varlen fallback.
+ * total_rows = cu_seqlens_k[num_requests] (host-known, sizes the launch).
+ */
+int32_t mi_gather_kv(const void* key_cache, const void* value_cache,
+                     int64_t cache_block_stride, int64_t cache_token_stride,
+                     int64_t cache_head_stride, const int32_t* block_tables,
+                     int64_t block_table_stride, int32_t block_table_width,
+                     const int32_t* cu_seqlens_k, int32_t num_requests, int32_t total_rows,
+                     void* key_out, void* value_out, int32_t num_kv_heads,
+                     int32_t head_dim, int32_t block_size, int32_t num_blocks,
+                     int32_t dtype, void* stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* MI_ATTN_H_ */

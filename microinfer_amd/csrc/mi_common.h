@@ -1,0 +1,125 @@
+// Shared device helpers for the gfx950 paged-KV kernels: element types,
+// 16-byte vector packs and 64-lane wavefront reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "mi_attn.h"
+
+namespace mi {
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+// ---------------------------------------------------------------------------
+// Element types. 16-bit floats travel as raw uint16_t bit patterns; all
+// arithmetic is float32.
+// ---------------------------------------------------------------------------
+struct F32 {
+  using raw = float;
+  static __device__ __forceinline__ float load(raw x) { return x; }
+  static __device__ __forceinline__ raw store(float x) { return x; }
+};
+
+struct BF16 {
+  using raw = uint16_t;
+  static __device__ __forceinline__ float load(raw x) {
+    return __uint_as_float(static_cast<uint32_t>(x) << 16);
+  }
+  // Round to nearest even; NaN becomes the canonical quiet NaN 0x7FC0.
+  static __device__ __forceinline__ raw store(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<raw>(u >> 16);
+  }
+};
+
+struct F16 {
+  using raw = uint16_t;
+  static __device__ __forceinline__ float load(raw x) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, x));
+  }
+  static __device__ __forceinline__ raw store(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  }
+};
+
+// N consecutive raw elements moved with one load/store instruction.
+template <typename R, int N>
+struct alignas(sizeof(R) * N) Pack {
+  R v[N];
+};
+
+template <typename R, int N>
+__device__ __forceinline__ Pack<R, N> load_pack(const R* p) {
+  return *reinterpret_cast<const Pack<R, N>*>(p);
+}
+
+template <typename R, int N>
+__device__ __forceinline__ void store_pack(R* p, const Pack<R, N>& v) {
+  *reinterpret_cast<Pack<R, N>*>(p) = v;
+}
+
+template <typename R, int N>
+__device__ __forceinline__ Pack<R, N> zero_pack() {
+  Pack<R, N> z;
+#pragma unroll
+  for (int i = 0; i < N; ++i) z.v[i] = R(0);
+  return z;
+}
+
+// ---------------------------------------------------------------------------
+// Wavefront reductions (xor butterflies; every participating lane ends with
+// the result).
+// ---------------------------------------------------------------------------
+template <int FROM, int TO>
+__device__ __forceinline__ float xor_sum(float v) {
+#pragma unroll
+  for (int o = FROM; o < TO; o <<= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+template <int FROM, int TO>
+__device__ __forceinline__ float xor_max(float v) {
+#pragma unroll
+  for (int o = FROM; o < TO; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    int t = __shfl_up(v, o, kWave);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+__host__ __device__ constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v >> 1); }
+
+inline bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+// ---------------------------------------------------------------------------
+// Host-side error reporting (thread-local, read through mi_last_error()).
+// ---------------------------------------------------------------------------
+void set_error(const std::string& msg);
+void clear_error();
+int32_t fail(int32_t status, const std::string& msg);
+int32_t check_launch(const char* what);
+
+inline size_t dtype_size(int32_t dtype) { return dtype == MI_DTYPE_F32 ? 4 : 2; }
+
+inline bool valid_dtype(int32_t dtype) {
+  return dtype == MI_DTYPE_F32 || dtype == MI_DTYPE_F16 || dtype == MI_DTYPE_BF16;
+}
+
+}  // namespace mi

@@ -1,0 +1,45 @@
+// Internal declarations shared by the paged-attention translation units.
+#pragma once
+
+#include "mi_common.h"
+
+namespace mi {
+
+// Arguments of the vector (non-MFMA) paged attention kernels. Strides are in
+// elements; head_dim is contiguous everywhere.
+struct AttnArgs {
+  const void* q;
+  int64_t q_ts, q_hs;
+  const void* kc;
+  const void* vc;
+  int64_t c_bs, c_ts, c_hs;
+  const int32_t* tables;
+  int64_t t_stride;
+  int32_t t_width;
+  const int32_t* ctx;   // decode: context length per sequence
+  const int32_t* cu_q;  // varlen: query row offsets [R + 1]
+  const int32_t* cu_k;  // varlen: context offsets [R + 1]
+  void* out;
+  int64_t o_ts, o_hs;
+  float* ws_acc;  // split partials: [items, Hkv, G, D] unnormalised sums
+  float* ws_ml;   // split partials: [items, Hkv, G, 2] (log2-domain max, sum)
+  int32_t num_seqs;  // decode: sequences; varlen: requests
+  int32_t num_rows;  // varlen: query rows
+  int32_t num_kv_heads, group, head_dim, block_size, log2_block, num_blocks;
+  int32_t split_k;          // 0 = adaptive partitions
+  int32_t target_items;     // adaptive: aim for about this many (item, head) groups
+  int32_t min_part_blocks;  // adaptive: smallest partition, in blocks
+  int32_t max_items;        // grid.x of the decode launch
+  float scale_log2;         // softmax scale * log2(e)
+  int32_t varlen;
+};
+
+// Launch the vector kernel (decode or varlen mode) plus, for decode, the
+// split merge. Returns an MI_* status.
+int32_t launch_paged_attention_vector(const AttnArgs& args, int32_t dtype,
+                                      hipStream_t stream);
+
+// Upper bound on decode work items for a launch (grid.x).
+int32_t decode_max_items(int32_t num_seqs, int32_t num_kv_heads, int32_t split_k);
+
+}  // namespace mi

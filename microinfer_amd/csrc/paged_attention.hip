@@ -1,0 +1,208 @@
+// C entry points for paged decode and paged varlen (prefill) attention.
+#include <cmath>
+
+#include "paged_attention.h"
+
+namespace mi {
+
+int32_t launch_vector_f32(const AttnArgs& a, hipStream_t stream);
+int32_t launch_vector_f16(const AttnArgs& a, hipStream_t stream);
+int32_t launch_vector_bf16(const AttnArgs& a, hipStream_t stream);
+
+namespace {
+
+// Adaptive split-K tuning: the decode launch aims for about kTargetItems
+// (work item, KV head) wavefronts, each covering at least kMinPartBlocks blocks.
+int32_t g_target_items = 2048;
+int32_t g_min_part_blocks = 2;
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+int32_t dispatch_vector(const AttnArgs& a, int32_t dtype, hipStream_t stream) {
+  switch (dtype) {
+    case MI_DTYPE_F32: return launch_vector_f32(a, stream);
+    case MI_DTYPE_F16: return launch_vector_f16(a, stream);
+    case MI_DTYPE_BF16: return launch_vector_bf16(a, stream);
+    default: return fail(MI_ERR_INVALID_ARGUMENT, "paged attention: bad dtype");
+  }
+}
+
+// Common shape/stride validation. `vec` elements must stay 16-byte loadable.
+int32_t check_common(const char* who, int32_t dtype, int32_t num_q_heads,
+                     int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                     int32_t num_blocks, int32_t table_width) {
+  if (!valid_dtype(dtype)) return fail(MI_ERR_INVALID_ARGUMENT, std::string(who) + ": bad dtype");
+  if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0)
+    return fail(MI_ERR_INVALID_ARGUMENT,
+                std::string(who) + ": Hq must be a positive multiple of Hkv");
+  if (!is_pow2(head_dim) || head_dim > 256)
+    return fail(MI_ERR_UNSUPPORTED,
+                std::string(who) + ": head_dim must be a power of two <= 256");
+  if (!is_pow2(block_size))
+    return fail(MI_ERR_INVALID_ARGUMENT,
+                std::string(who) + ": block_size must be a power of two");
+  if (num_blocks <= 0 || table_width < 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, std::string(who) + ": invalid pool or table size");
+  return MI_OK;
+}
+
+bool aligned(const void* p, int64_t bytes) {
+  return (reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(bytes)) == 0;
+}
+
+}  // namespace
+
+int32_t decode_max_items(int32_t num_seqs, int32_t num_kv_heads, int32_t split_k) {
+  if (split_k > 0) return num_seqs * split_k;
+  return (g_target_items + num_kv_heads - 1) / num_kv_heads + num_seqs;
+}
+
+}  // namespace mi
+
+extern "C" void mi_tune_decode(int32_t target_items, int32_t min_part_blocks) {
+  if (target_items > 0) mi::g_target_items = target_items;
+  if (min_part_blocks > 0) mi::g_min_part_blocks = min_part_blocks;
+}
+
+extern "C" int64_t mi_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
+                                                   int32_t num_kv_heads, int32_t head_dim,
+                                                   int32_t split_k) {
+  if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || head_dim <= 0 || split_k < 0)
+    return 0;
+  if (split_k == 1) return 0;  // one partition per sequence: no partials
+  const int64_t items = mi::decode_max_items(num_seqs, num_kv_heads, split_k);
+  const int64_t group = num_q_heads / num_kv_heads;
+  return items * num_kv_heads * group * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
+}
+
+extern "C" int32_t mi_paged_decode(
+    const void* query, int64_t q_token_stride, int64_t q_head_stride, const void* key_cache,
+    const void* value_cache, int64_t cache_block_stride, int64_t cache_token_stride,
+    int64_t cache_head_stride, const int32_t* block_tables, int64_t block_table_stride,
+    int32_t block_table_width, const int32_t* context_lens, void* out,
+    int64_t out_token_stride, int64_t out_head_stride, void* workspace,
+    int64_t workspace_bytes, int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int32_t num_blocks, int32_t split_k, float scale,
+    int32_t dtype, void* stream) {
+  using namespace mi;
+  clear_error();
+  int32_t st = check_common("mi_paged_decode", dtype, num_q_heads, num_kv_heads, head_dim,
+                            block_size, num_blocks, block_table_width);
+  if (st != MI_OK) return st;
+  if (num_seqs < 0 || split_k < 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode: negative num_seqs or split_k");
+  if (num_seqs == 0) return MI_OK;
+  if (!query || !key_cache || !value_cache || !block_tables || !context_lens || !out)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode: null pointer");
+  const int64_t es = static_cast<int64_t>(dtype_size(dtype));
+  const int64_t vec = std::min<int64_t>(head_dim, 16 / es);
+  const int64_t vb = vec * es;
+  if (!aligned(query, vb) || !aligned(key_cache, vb) || !aligned(value_cache, vb) ||
+      !aligned(out, vb) || q_token_stride % vec || q_head_stride % vec ||
+      cache_block_stride % vec || cache_token_stride % vec || cache_head_stride % vec ||
+      out_token_stride % vec || out_head_stride % vec)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode: misaligned pointers or strides");
+  const int64_t need = mi_paged_decode_workspace_bytes(num_seqs, num_q_heads, num_kv_heads,
+                                                       head_dim, split_k);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 256)))
+    return fail(MI_ERR_WORKSPACE, "mi_paged_decode: workspace needs " +
+                                      std::to_string(need) + " bytes (256-byte aligned)");
+
+  AttnArgs a{};
+  a.q = query;
+  a.q_ts = q_token_stride;
+  a.q_hs = q_head_stride;
+  a.kc = key_cache;
+  a.vc = value_cache;
+  a.c_bs = cache_block_stride;
+  a.c_ts = cache_token_stride;
+  a.c_hs = cache_head_stride;
+  a.tables = block_tables;
+  a.t_stride = block_table_stride;
+  a.t_width = block_table_width;
+  a.ctx = context_lens;
+  a.out = out;
+  a.o_ts = out_token_stride;
+  a.o_hs = out_head_stride;
+  a.num_seqs = num_seqs;
+  a.num_kv_heads = num_kv_heads;
+  a.group = num_q_heads / num_kv_heads;
+  a.head_dim = head_dim;
+  a.block_size = block_size;
+  a.log2_block = ilog2(block_size);
+  a.num_blocks = num_blocks;
+  a.split_k = split_k;
+  a.target_items = g_target_items;
+  a.min_part_blocks = g_min_part_blocks;
+  a.max_items = decode_max_items(num_seqs, num_kv_heads, split_k == 1 ? 1 : split_k);
+  a.scale_log2 = scale * kLog2e;
+  a.varlen = 0;
+  if (need > 0) {
+    const int64_t acc_floats =
+        static_cast<int64_t>(a.max_items) * num_kv_heads * a.group * head_dim;
+    a.ws_acc = static_cast<float*>(workspace);
+    a.ws_ml = a.ws_acc + acc_floats;
+  }
+  return dispatch_vector(a, dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t mi_paged_prefill(
+    const void* query, int64_t q_token_stride, int64_t q_head_stride, const void* key_cache,
+    const void* value_cache, int64_t cache_block_stride, int64_t cache_token_stride,
+    int64_t cache_head_stride, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+    const int32_t* block_tables, int64_t block_table_stride, int32_t block_table_width,
+    void* out, int64_t out_token_stride, int64_t out_head_stride, int32_t num_tokens,
+    int32_t num_requests, int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int32_t num_blocks, float scale, int32_t dtype,
+    void* stream) {
+  using namespace mi;
+  clear_error();
+  int32_t st = check_common("mi_paged_prefill", dtype, num_q_heads, num_kv_heads, head_dim,
+                            block_size, num_blocks, block_table_width);
+  if (st != MI_OK) return st;
+  if (num_tokens < 0 || num_requests < 0 || max_seqlen_q < 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_prefill: negative sizes");
+  if (num_tokens == 0) return MI_OK;
+  if (num_requests == 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_prefill: tokens without requests");
+  // block_tables may be NULL: contiguous varlen K/V (see mi_attn.h).
+  if (!query || !key_cache || !value_cache || !cu_seqlens_q || !cu_seqlens_k || !out)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_prefill: null pointer");
+  const int64_t es = static_cast<int64_t>(dtype_size(dtype));
+  const int64_t vec = std::min<int64_t>(head_dim, 16 / es);
+  const int64_t vb = vec * es;
+  if (!aligned(query, vb) || !aligned(key_cache, vb) || !aligned(value_cache, vb) ||
+      !aligned(out, vb) || q_token_stride % vec || q_head_stride % vec ||
+      cache_block_stride % vec || cache_token_stride % vec || cache_head_stride % vec ||
+      out_token_stride % vec || out_head_stride % vec)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_prefill: misaligned pointers or strides");
+
+  AttnArgs a{};
+  a.q = query;
+  a.q_ts = q_token_stride;
+  a.q_hs = q_head_stride;
+  a.kc = key_cache;
+  a.vc = value_cache;
+  a.c_bs = cache_block_stride;
+  a.c_ts = cache_token_stride;
+  a.c_hs = cache_head_stride;
+  a.tables = block_tables;
+  a.t_stride = block_table_stride;
+  a.t_width = block_table_width;
+  a.cu_q = cu_seqlens_q;
+  a.cu_k = cu_seqlens_k;
+  a.out = out;
+  a.o_ts = out_token_stride;
+  a.o_hs = out_head_stride;
+  a.num_seqs = num_requests;
+  a.num_rows = num_tokens;
+  a.num_kv_heads = num_kv_heads;
+  a.group = num_q_heads / num_kv_heads;
+  a.head_dim = head_dim;
+  a.block_size = block_size;
+  a.log2_block = ilog2(block_size);
+  a.num_blocks = num_blocks;
+  a.scale_log2 = scale * kLog2e;
+  a.varlen = 1;
+  return dispatch_vector(a, dtype, static_cast<hipStream_t>(stream));
+}

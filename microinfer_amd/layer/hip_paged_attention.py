@@ -1,0 +1,266 @@
+"""HIP paged attention ops for gfx950, called through libmi_attn.so.
+
+Drop-ins for the reference's Triton entry points
+(microinfer/layer/triton_paged_attention.py):
+
+* ``hip_paged_decode``  <- ``triton_paged_decode``  (:352-457)
+* ``hip_paged_prefill`` <- ``triton_paged_prefill`` (:260-339)
+
+Same positional/keyword arguments, same ValueError checks (:280-302,
+:370-399), same output dtype and shape. Differences by design:
+
+* One launch handles all G = Hq/Hkv query heads of a KV head, so K/V is read
+  from HBM once per step (the reference reads it G times).
+* ``split_k=None`` plans context partitions on the device from
+  ``context_lens`` (the reference picks 4 or 1 on the host from R*Hq); an int
+  forces at most that many partitions per sequence. The launch shape depends
+  only on the batch size, so hipGraph capture stays valid as contexts grow.
+* Prefill also accepts float32 (vector kernel) and contiguous varlen K/V
+  (``block_tables=None``), which serves the no-prefix prefill.
+
+Workspace comes from torch's caching allocator (the graph pool under
+capture); the library never allocates.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from microinfer_amd import _lib
+
+_FLOAT_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def _is_pow2(value: int) -> bool:
+    return value > 0 and value & (value - 1) == 0
+
+
+def _inner_contiguous(tensor: torch.Tensor) -> torch.Tensor:
+    return tensor if tensor.stride(-1) == 1 else tensor.contiguous()
+
+
+def _index32(tensor: torch.Tensor) -> torch.Tensor:
+    if tensor.dtype != torch.int32:
+        tensor = tensor.to(torch.int32)
+    return tensor.contiguous()
+
+
+def _check_caches(key_cache: torch.Tensor, value_cache: torch.Tensor):
+    if key_cache.ndim != 4 or value_cache.shape != key_cache.shape:
+        raise ValueError("key/value caches must have matching [blocks, B, Hkv, D] shapes")
+    if value_cache.dtype != key_cache.dtype or value_cache.device != key_cache.device:
+        raise ValueError("key/value caches must share dtype and device")
+    key_cache = _inner_contiguous(key_cache)
+    value_cache = _inner_contiguous(value_cache)
+    if key_cache.stride() != value_cache.stride():
+        # The kernels address K and V with one set of strides.
+        key_cache = key_cache.contiguous()
+        value_cache = value_cache.contiguous()
+    return key_cache, value_cache
+
+
+def decode_workspace_bytes(num_seqs: int, num_q_heads: int, num_kv_heads: int,
+                           head_dim: int, split_k: int | None) -> int:
+    return int(
+        _lib.load().mi_paged_decode_workspace_bytes(
+            num_seqs, num_q_heads, num_kv_heads, head_dim, 0 if split_k is None else split_k
+        )
+    )
+
+
+def hip_paged_decode(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    *,
+    scale: float | None = None,
+    split_k: int | None = None,
+) -> torch.Tensor:
+    """Decode one query row per request over the paged cache.
+
+    ``query [R, Hq, D]``, caches ``[N, B, Hkv, D]`` (any strides with D
+    contiguous), ``block_tables [R, W]`` and ``context_lens [R]`` on the device.
+    Returns ``[R, Hq, D]`` in the query dtype.
+    """
+    if query.ndim != 3:
+        raise ValueError("query must have shape [requests, Hq, D]")
+    num_requests, num_q_heads, head_dim = query.shape
+    if key_cache.ndim != 4:
+        raise ValueError("key_cache must have shape [blocks, B, Hkv, D]")
+    num_blocks, block_size, num_kv_heads, kv_dim = key_cache.shape
+    if num_requests == 0:
+        return torch.empty_like(query)
+    if query.device != key_cache.device or query.dtype != key_cache.dtype:
+        raise ValueError("query and cache must share device/dtype")
+    if not query.is_cuda:
+        raise ValueError("HIP paged decode requires a GPU device")
+    if query.dtype not in _FLOAT_DTYPES:
+        raise ValueError("unsupported query dtype")
+    if kv_dim != head_dim:
+        raise ValueError("query and cache head dimensions differ")
+    if num_q_heads % num_kv_heads:
+        raise ValueError("Hq must be divisible by Hkv")
+    if not _is_pow2(block_size):
+        raise ValueError("paged kernels require a power-of-two block size")
+    if not _is_pow2(head_dim):
+        raise ValueError("paged kernels require a power-of-two head_dim")
+    if split_k is not None and (type(split_k) is not int or not _is_pow2(split_k)):
+        raise ValueError("split_k must be a positive power of two")
+    if block_tables.ndim != 2 or block_tables.shape[0] != num_requests:
+        raise ValueError("block_tables must have one row per request")
+    if context_lens.numel() != num_requests:
+        raise ValueError("context_lens must have one entry per request")
+    _lib.require_device(block_tables, context_lens, what="hip_paged_decode")
+
+    key_cache, value_cache = _check_caches(key_cache, value_cache)
+    query = _inner_contiguous(query)
+    block_tables = _index32(block_tables)
+    context_lens = _index32(context_lens)
+    output = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+
+    lib = _lib.load()
+    split = 0 if split_k is None else split_k
+    ws_bytes = int(
+        lib.mi_paged_decode_workspace_bytes(
+            num_requests, num_q_heads, num_kv_heads, head_dim, split
+        )
+    )
+    workspace = (
+        torch.empty(ws_bytes, dtype=torch.uint8, device=query.device) if ws_bytes else None
+    )
+    status = lib.mi_paged_decode(
+        query.data_ptr(), query.stride(0), query.stride(1),
+        key_cache.data_ptr(), value_cache.data_ptr(),
+        key_cache.stride(0), key_cache.stride(1), key_cache.stride(2),
+        block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
+        context_lens.data_ptr(),
+        output.data_ptr(), output.stride(0), output.stride(1),
+        None if workspace is None else workspace.data_ptr(), ws_bytes,
+        num_requests, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
+        split, float(scale), _lib.dtype_code(query.dtype),
+        _lib.stream_handle(query.device),
+    )
+    _lib.check(status, "mi_paged_decode")
+    return output
+
+
+def hip_paged_prefill(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    cu_seqlens_k: torch.Tensor,
+    block_tables: torch.Tensor | None,
+    *,
+    max_seqlen_q: int,
+    scale: float | None = None,
+) -> torch.Tensor:
+    """Causal varlen attention straight from the paged cache (bottom-right mask).
+
+    ``query [T, Hq, D]``; request r owns query rows ``cu_seqlens_q[r]..`` and
+    context ``cu_seqlens_k[r+1] - cu_seqlens_k[r]`` (it includes the new rows,
+    which the caller appended first). With ``block_tables=None`` the "caches"
+    are contiguous ``[sum c, Hkv, D]`` K/V and request r's keys start at row
+    ``cu_seqlens_k[r]``.
+    """
+    if query.ndim != 3:
+        raise ValueError("query must have shape [tokens, Hq, D]")
+    num_tokens, num_q_heads, head_dim = query.shape
+    paged = block_tables is not None
+    if paged:
+        if key_cache.ndim != 4:
+            raise ValueError("key_cache must have shape [blocks, B, Hkv, D]")
+        num_blocks, block_size, num_kv_heads, kv_dim = key_cache.shape
+        num_requests = block_tables.shape[0]
+    else:
+        if key_cache.ndim != 3 or value_cache.shape != key_cache.shape:
+            raise ValueError("contiguous K/V must have shape [rows, Hkv, D]")
+        num_blocks, num_kv_heads, kv_dim = key_cache.shape
+        block_size = 1
+        num_requests = cu_seqlens_q.numel() - 1
+    if num_tokens == 0 or num_requests == 0:
+        return torch.empty_like(query)
+    if query.device != key_cache.device or query.dtype != key_cache.dtype:
+        raise ValueError("query and cache must share device/dtype")
+    if not query.is_cuda:
+        raise ValueError("HIP paged prefill requires a GPU device")
+    if query.dtype not in _FLOAT_DTYPES:
+        raise ValueError("unsupported query dtype")
+    if kv_dim != head_dim or not _is_pow2(head_dim):
+        raise ValueError("head dimension must match and be a power of two")
+    if num_q_heads % num_kv_heads:
+        raise ValueError("Hq must be divisible by Hkv")
+    if not _is_pow2(block_size):
+        raise ValueError("paged kernels require a power-of-two block size")
+    if cu_seqlens_q.numel() != num_requests + 1:
+        raise ValueError("cu_seqlens_q must have num_requests + 1 entries")
+    if cu_seqlens_k.numel() != num_requests + 1:
+        raise ValueError("cu_seqlens_k must have num_requests + 1 entries")
+    if max_seqlen_q <= 0:
+        raise ValueError("max_seqlen_q must be positive")
+    _lib.require_device(cu_seqlens_q, cu_seqlens_k, block_tables, what="hip_paged_prefill")
+
+    query = _inner_contiguous(query)
+    if paged:
+        key_cache, value_cache = _check_caches(key_cache, value_cache)
+        block_tables = _index32(block_tables)
+        c_bs, c_ts, c_hs = key_cache.stride(0), key_cache.stride(1), key_cache.stride(2)
+        t_ptr, t_stride, t_width = block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1]
+    else:
+        key_cache = _inner_contiguous(key_cache)
+        value_cache = _inner_contiguous(value_cache)
+        if key_cache.stride() != value_cache.stride():
+            key_cache, value_cache = key_cache.contiguous(), value_cache.contiguous()
+        c_bs, c_ts, c_hs = 0, key_cache.stride(0), key_cache.stride(1)
+        t_ptr, t_stride, t_width = None, 0, 0
+        # The kernel never reads past this many K/V rows.
+        num_blocks = max(num_blocks, 1)
+    cu_seqlens_q = _index32(cu_seqlens_q)
+    cu_seqlens_k = _index32(cu_seqlens_k)
+    output = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+
+    status = _lib.load().mi_paged_prefill(
+        query.data_ptr(), query.stride(0), query.stride(1),
+        key_cache.data_ptr(), value_cache.data_ptr(), c_bs, c_ts, c_hs,
+        cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), t_ptr, t_stride, t_width,
+        output.data_ptr(), output.stride(0), output.stride(1),
+        num_tokens, num_requests, int(max_seqlen_q), num_q_heads, num_kv_heads, head_dim,
+        block_size, num_blocks, float(scale), _lib.dtype_code(query.dtype),
+        _lib.stream_handle(query.device),
+    )
+    _lib.check(status, "mi_paged_prefill")
+    return output
+
+
+def hip_gather_kv(key_cache, value_cache, block_tables, cu_seqlens_k, total_rows: int):
+    """One-launch gather of each request's valid rows into contiguous K/V."""
+    _lib.require_device(key_cache, value_cache, block_tables, cu_seqlens_k, what="gather_kv")
+    key_cache, value_cache = _check_caches(key_cache, value_cache)
+    num_blocks, block_size, num_kv_heads, head_dim = key_cache.shape
+    if not _is_pow2(block_size):
+        raise ValueError("paged kernels require a power-of-two block size")
+    block_tables = _index32(block_tables)
+    cu_seqlens_k = _index32(cu_seqlens_k)
+    shape = (total_rows, num_kv_heads, head_dim)
+    keys = torch.empty(shape, dtype=key_cache.dtype, device=key_cache.device)
+    values = torch.empty_like(keys)
+    if total_rows == 0:
+        return keys, values
+    status = _lib.load().mi_gather_kv(
+        key_cache.data_ptr(), value_cache.data_ptr(),
+        key_cache.stride(0), key_cache.stride(1), key_cache.stride(2),
+        block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
+        cu_seqlens_k.data_ptr(), block_tables.shape[0], total_rows,
+        keys.data_ptr(), values.data_ptr(), num_kv_heads, head_dim, block_size, num_blocks,
+        _lib.dtype_code(key_cache.dtype), _lib.stream_handle(key_cache.device),
+    )
+    _lib.check(status, "mi_gather_kv")
+    return keys, values

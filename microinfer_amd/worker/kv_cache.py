@@ -1,0 +1,135 @@
+"""Runner-owned paged KV storage and zero-copy per-layer views.
+
+Mirrors ``LayerKVCache`` / ``KVCache`` (microinfer/worker/kv_cache.py:10-118):
+same constructor, ``layer(i)``, ``num_bytes``, ``keys``/``values`` and
+``write_checked``/``write_fast`` contracts. Two things differ by design:
+
+* Physical layout. Storage is allocated head-major, ``[L, N, Hkv, B, D]``, so
+  one KV head's 16-token block is one contiguous run (4 KiB in bf16 at
+  D=128) instead of 16 runs 2 KiB apart. ``keys``/``values`` are permuted
+  views with the reference's logical shape ``[L, N, B, Hkv, D]``, so indexing
+  (``cache.keys[l, blk, off]``) reads exactly what the reference would; the
+  kernels take the view's strides. ``layout="token_major"`` allocates the
+  reference's contiguous layout instead.
+* Writes run on the GPU only (no advanced-indexing CPU fallback,
+  kv_cache.py:78-79); a CPU cache can be built and validated but not written.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from microinfer_amd.worker.hip_kv_store import launch_append
+
+LAYOUTS = ("head_major", "token_major")
+
+
+@dataclass(frozen=True)
+class LayerKVCache:
+    """One layer's logical ``[blocks, B, Hkv, D]`` K/V views; no pool or layer id."""
+
+    keys: torch.Tensor
+    values: torch.Tensor
+
+    def __post_init__(self):
+        if self.keys.ndim != 4 or self.keys.shape != self.values.shape:
+            raise ValueError("K/V must have matching [blocks, B, Hkv, D] shapes")
+        if self.keys.dtype != self.values.dtype or self.keys.device != self.values.device:
+            raise ValueError("K/V must have matching dtype and device")
+
+    @property
+    def block_size(self):
+        return self.keys.shape[1]
+
+    def write_checked(self, slots, keys, values):
+        """Checked write (kv_cache.py:30-50): -1 skips padding; validates first.
+
+        Every check runs before any storage changes, so an invalid write leaves
+        the cache untouched.
+        """
+        if slots.ndim != 1 or slots.dtype not in (torch.int32, torch.int64):
+            raise ValueError("slots must be a 1-D integer tensor")
+        expected = (slots.numel(), *self.keys.shape[2:])
+        if keys.shape != expected or values.shape != expected:
+            raise ValueError("K/V shape must match slots and cache heads")
+        if any(t.device != self.keys.device for t in (slots, keys, values)):
+            raise ValueError("slots and K/V must be on the cache device")
+        capacity = self.keys.shape[0] * self.block_size
+        if bool(torch.any(slots < -1)) or bool(torch.any(slots >= capacity)):
+            raise ValueError("slot outside cache")
+        used = slots[slots >= 0].long()
+        if used.unique().numel() != used.numel():
+            raise ValueError("duplicate slot")
+        if slots.numel() == 0:
+            return
+        keys = keys.to(self.keys.dtype)
+        values = values.to(self.values.dtype)
+        launch_append(self.keys, self.values, slots, None, keys, values)
+
+    def write_fast(self, blocks, offsets, keys, values):
+        """Hot path (kv_cache.py:52-79): caller guarantees valid, unique slots."""
+        launch_append(self.keys, self.values, blocks, offsets, keys, values)
+
+    def write_slots(self, slot_mapping, keys, values):
+        """Hot path with the step's int32 slot map; -1 entries are skipped.
+
+        Duplicate slots are allowed (graph pad rows share the pad block);
+        which duplicate lands is unspecified.
+        """
+        launch_append(self.keys, self.values, slot_mapping, None, keys, values)
+
+
+class KVCache:
+    """KV pool for every layer, logical shape ``[L, N, B, Hkv, D]`` (zeros)."""
+
+    def __init__(
+        self,
+        num_layers,
+        num_blocks,
+        block_size,
+        num_kv_heads,
+        head_dim,
+        *,
+        dtype=torch.float32,
+        device="cpu",
+        layout: str = "head_major",
+    ):
+        dimensions = (num_layers, num_blocks, block_size, num_kv_heads, head_dim)
+        if any(d <= 0 for d in dimensions):
+            raise ValueError("cache dimensions must be positive")
+        if layout not in LAYOUTS:
+            raise ValueError(f"layout must be one of {LAYOUTS}")
+        self.num_layers = num_layers
+        self.num_blocks = num_blocks
+        self.block_size = block_size
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.layout = layout
+        if layout == "head_major":
+            physical = (num_layers, num_blocks, num_kv_heads, block_size, head_dim)
+            self._key_storage = torch.zeros(physical, dtype=dtype, device=device)
+            self._value_storage = torch.zeros_like(self._key_storage)
+            self.keys = self._key_storage.permute(0, 1, 3, 2, 4)
+            self.values = self._value_storage.permute(0, 1, 3, 2, 4)
+        else:
+            self._key_storage = torch.zeros(dimensions, dtype=dtype, device=device)
+            self._value_storage = torch.zeros_like(self._key_storage)
+            self.keys = self._key_storage
+            self.values = self._value_storage
+
+    @property
+    def num_bytes(self):
+        return (
+            self.keys.numel() * self.keys.element_size()
+            + self.values.numel() * self.values.element_size()
+        )
+
+    def layer(self, index: int) -> LayerKVCache:
+        """Basic indexing shares storage; binding does not copy the cache."""
+        if not 0 <= index < self.num_layers:
+            raise ValueError("layer outside cache")
+        return LayerKVCache(self.keys[index], self.values[index])

@@ -1,0 +1,85 @@
+"""The C-ABI library loads and exports what include/mi_attn.h declares.
+
+No kernel is launched here: argument validation returns before any HIP call,
+so these run on a host without a GPU.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from microinfer_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "mi_attn.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(mi_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 8
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_abi_version_and_clean_error_state():
+    lib = _lib.load()
+    assert lib.mi_abi_version() == 100
+    assert isinstance(_lib.last_error(), str)
+
+
+def test_invalid_arguments_fail_before_launch():
+    lib = _lib.load()
+    status = lib.mi_kv_append(None, 0, 0, None, 0, 0, None, None, 0, 0, 0, None, None, 0,
+                              1, 1, 8, 16, 4, 9, None)
+    assert status == 1 and "dtype" in _lib.last_error()
+    status = lib.mi_paged_decode(None, 0, 0, None, None, 0, 0, 0, None, 0, 1, None, None, 0, 0,
+                                 None, 0, 1, 3, 2, 128, 16, 4, 0, 1.0, 2, None)
+    assert status == 1 and "multiple" in _lib.last_error()
+    status = lib.mi_paged_decode(None, 0, 0, None, None, 0, 0, 0, None, 0, 1, None, None, 0, 0,
+                                 None, 0, 1, 4, 2, 96, 16, 4, 0, 1.0, 2, None)
+    assert status == 2 and "head_dim" in _lib.last_error()
+    status = lib.mi_paged_prefill(None, 0, 0, None, None, 0, 0, 0, None, None, None, 0, 1,
+                                  None, 0, 0, 4, 1, 4, 4, 2, 128, 12, 4, 1.0, 2, None)
+    assert status == 1 and "block_size" in _lib.last_error()
+    status = lib.mi_gather_kv(None, None, 0, 0, 0, None, 0, 1, None, 0, 5, None, None, 2, 128,
+                              16, 4, 2, None)
+    assert status == 1 and "requests" in _lib.last_error()
+
+
+def test_empty_work_is_a_no_op():
+    lib = _lib.load()
+    assert lib.mi_kv_append(None, 0, 0, None, 0, 0, None, None, 0, 0, 0, None, None, 0,
+                            0, 8, 128, 16, 4, 2, None) == 0
+    assert lib.mi_paged_decode(None, 0, 0, None, None, 0, 0, 0, None, 0, 1, None, None, 0, 0,
+                               None, 0, 0, 16, 8, 128, 16, 4, 0, 1.0, 2, None) == 0
+
+
+def test_missing_workspace_is_reported():
+    lib = _lib.load()
+    need = lib.mi_paged_decode_workspace_bytes(32, 16, 8, 128, 0)
+    assert need > 0
+    fake = ctypes.c_void_p(256)
+    status = lib.mi_paged_decode(fake, 2048, 128, fake, fake, 16384, 1024, 128, fake, 128, 128,
+                                 fake, fake, 2048, 128, None, 0, 32, 16, 8, 128, 16, 4096, 0,
+                                 1.0, 2, None)
+    assert status == 3 and "workspace" in _lib.last_error()
+
+
+@pytest.mark.parametrize("split_k,expect_zero", [(1, True), (0, False), (4, False)])
+def test_workspace_size_formula(split_k, expect_zero):
+    lib = _lib.load()
+    size = lib.mi_paged_decode_workspace_bytes(4, 32, 8, 128, split_k)
+    if expect_zero:
+        assert size == 0
+    elif split_k:
+        assert size == 4 * split_k * 8 * 4 * (128 + 2) * 4
+    else:
+        assert size % (8 * 4 * 130 * 4) == 0
