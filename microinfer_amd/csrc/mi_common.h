@@ -89,6 +89,28 @@ __device__ __forceinline__ float xor_max(float v) {
   return v;
 }
 
+// DPP lane move within a 16-lane row (bound_ctrl off: every source used here
+// is a valid lane). CTRL values: 0xB1 quad_perm[1,0,3,2] (xor 1),
+// 0x4E quad_perm[2,3,0,1] (xor 2), 0x141 row_half_mirror, 0x140 row_mirror.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of N lanes; every lane of a group gets the sum.
+// Groups of up to 16 lanes reduce with DPP (no LDS traffic).
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (N >= 2) v += dpp_move<0xB1>(v);
+  if constexpr (N >= 4) v += dpp_move<0x4E>(v);
+  if constexpr (N >= 8) v += dpp_move<0x141>(v);
+  if constexpr (N >= 16) v += dpp_move<0x140>(v);
+  if constexpr (N >= 32) v += __shfl_xor(v, 16, kWave);
+  if constexpr (N >= 64) v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
 __device__ __forceinline__ int wave_sum_int(int v) {
 #pragma unroll
   for (int o = 1; o < kWave; o <<= 1) v += __shfl_xor(v, o, kWave);

@@ -128,12 +128,13 @@ __global__ __launch_bounds__(kWave) void paged_attention_vector_kernel(const Att
   } else {
     WorkItem it;
     if (!decode_plan(a, w, false, lane, it)) return;
-    seq = it.seq;
-    q_row = it.seq;
-    ctx = it.ctx;
-    blk_begin = it.blk_begin;
-    blk_end = it.blk_end;
-    nparts = it.nparts;
+    // The plan is identical on every lane; keep it in scalar registers.
+    seq = __builtin_amdgcn_readfirstlane(it.seq);
+    q_row = seq;
+    ctx = __builtin_amdgcn_readfirstlane(it.ctx);
+    blk_begin = __builtin_amdgcn_readfirstlane(it.blk_begin);
+    blk_end = __builtin_amdgcn_readfirstlane(it.blk_end);
+    nparts = __builtin_amdgcn_readfirstlane(it.nparts);
   }
 
   // Query rows of the G heads, pre-scaled into the log2 domain.
@@ -162,89 +163,123 @@ __global__ __launch_bounds__(kWave) void paged_attention_vector_kernel(const Att
 
   const R* kc = static_cast<const R*>(a.kc);
   const R* vc = static_cast<const R*>(a.vc);
-  const int64_t head_off = head * a.c_hs + d0;
   // Contiguous mode (varlen only, no block table): request `seq` owns K/V rows
-  // cu_k[seq] .. cu_k[seq + 1] - 1 of a [rows, Hkv, D] array.
+  // cu_k[seq] .. cu_k[seq + 1] - 1 of a [rows, Hkv, D] array; num_blocks holds
+  // the row count. It runs as one "block" that spans the whole request.
   const bool paged = a.tables != nullptr;
   const int32_t* trow = paged ? a.tables + seq * a.t_stride : nullptr;
   const int64_t row0 = paged ? 0 : a.cu_k[seq];
-  const int bmask = a.block_size - 1;
-  const int pos_begin = paged ? blk_begin << a.log2_block : 0;
-  const int pos_end = paged ? min(ctx, blk_end << a.log2_block) : ctx;
+  const int lb = paged ? a.log2_block : 30;
+  const int bmask = paged ? a.block_size - 1 : (1 << 30) - 1;
+  const int64_t base_off = head * a.c_hs + d0 + row0 * a.c_ts;
+  // Any in-bounds address; masked rows load from here and are discarded.
+  const int64_t safe_off = head * a.c_hs + d0;
+  int pos_begin, pos_end;
+  if (paged) {
+    pos_begin = blk_begin << lb;
+    pos_end = min(ctx, blk_end << lb);
+  } else {
+    pos_begin = 0;
+    pos_end = static_cast<int>(min<int64_t>(ctx, max<int64_t>(a.num_blocks - row0, 0)));
+    blk_end = 1;
+  }
+  // A load instruction covers PPW consecutive positions; when PPW <= B they
+  // always share one block, so its id is wave-uniform and read with readlane.
+  const bool uniform_ids = !paged || PPW <= a.block_size;
 
-  for (int t0 = pos_begin; t0 < pos_end; t0 += TILE) {
-    Pack<R, VEC> kp[UNROLL], vp[UNROLL];
-    bool ok[UNROLL];
+  // Block ids of up to 64 blocks live in registers (one per lane).
+  for (int chunk = blk_begin; chunk < blk_end; chunk += kWave) {
+    const int cpos_begin = paged ? max(pos_begin, chunk << lb) : pos_begin;
+    const int cpos_end = paged ? min(pos_end, (chunk + kWave) << lb) : pos_end;
+    if (cpos_begin >= cpos_end) break;
+    int my_blk = 0;
+    if (paged) {
+      const int b = chunk + lane;
+      my_blk = b < blk_end ? trow[b] : -1;
+    }
+
+    for (int t0 = cpos_begin; t0 < cpos_end; t0 += TILE) {
+      int64_t off[UNROLL];
+      bool ok[UNROLL];
+      if (uniform_ids) {
+        // Block address is scalar; each lane adds its row and column.
+        const int64_t lane_off = grp * a.c_ts + base_off;
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const int pos = t0 + u * PPW + grp;
-      int64_t off = 0;
-      ok[u] = false;
-      if (pos < pos_end) {
-        if (paged) {
-          const int blk = trow[pos >> a.log2_block];
-          ok[u] = blk >= 0 && blk < a.num_blocks;
-          off = blk * a.c_bs + (pos & bmask) * a.c_ts + head_off;
-        } else {
-          // num_blocks holds the K/V row count in contiguous mode.
-          ok[u] = row0 + pos < a.num_blocks;
-          off = (row0 + pos) * a.c_ts + head_off;
+        for (int u = 0; u < UNROLL; ++u) {
+          const int p0 = t0 + u * PPW;
+          const int blk = __builtin_amdgcn_readlane(my_blk, ((p0 >> lb) - chunk) & (kWave - 1));
+          const bool blk_ok = blk >= 0 && blk < a.num_blocks;
+          const int64_t block_off = blk * a.c_bs + (p0 & bmask) * a.c_ts;
+          ok[u] = blk_ok && p0 + grp < cpos_end;
+          off[u] = ok[u] ? block_off + lane_off : safe_off;
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+          const int pos = t0 + u * PPW + grp;
+          const int blk = __shfl(my_blk, ((pos >> lb) - chunk) & (kWave - 1), kWave);
+          ok[u] = pos < cpos_end && blk >= 0 && blk < a.num_blocks;
+          off[u] = ok[u] ? blk * a.c_bs + (pos & bmask) * a.c_ts + base_off : safe_off;
         }
       }
-      if (ok[u]) {
-        kp[u] = load_pack<R, VEC>(kc + off);
-        vp[u] = load_pack<R, VEC>(vc + off);
-      } else {
-        kp[u] = zero_pack<R, VEC>();
-        vp[u] = zero_pack<R, VEC>();
-      }
-    }
+      // Issue every K and V load of the tile before any arithmetic.
+      Pack<R, VEC> kp[UNROLL], vp[UNROLL];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) kp[u] = load_pack<R, VEC>(kc + off[u]);
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) vp[u] = load_pack<R, VEC>(vc + off[u]);
 
-    float s[UNROLL][GMAX];
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      float kf[VEC];
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) kf[j] = E::load(kp[u].v[j]);
-#pragma unroll
-      for (int g = 0; g < GMAX; ++g) {
-        float dot = 0.f;
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) dot = fmaf(qf[g][j], kf[j], dot);
-        dot = xor_sum<1, LPR>(dot);
-        s[u][g] = ok[u] ? dot : -INFINITY;
-      }
-    }
-
-#pragma unroll
-    for (int g = 0; g < GMAX; ++g) {
-      if (!EXACT && g >= G) continue;
-      float tmax = s[0][g];
-#pragma unroll
-      for (int u = 1; u < UNROLL; ++u) tmax = fmaxf(tmax, s[u][g]);
-      tmax = xor_max<LPR, kWave>(tmax);
-      const float mnew = fmaxf(m[g], tmax);
-      const float alpha = (mnew == -INFINITY) ? 1.f : exp2f(m[g] - mnew);
-      m[g] = mnew;
-      lsum[g] *= alpha;
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) acc[g][j] *= alpha;
+      // Scores of this lane group's UNROLL positions.
+      float s[UNROLL][GMAX];
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) {
-        const float p = ok[u] ? exp2f(s[u][g] - mnew) : 0.f;
-        lsum[g] += p;
+        float kf[VEC];
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) acc[g][j] = fmaf(p, E::load(vp[u].v[j]), acc[g][j]);
+        for (int j = 0; j < VEC; ++j) kf[j] = E::load(kp[u].v[j]);
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+          float dot = 0.f;
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) dot = fmaf(qf[g][j], kf[j], dot);
+          dot = group_sum<LPR>(dot);
+          s[u][g] = ok[u] ? dot : -INFINITY;
+        }
+      }
+
+      // Online softmax per lane group (each group is its own split; groups
+      // are merged once at the end), then P.V.
+#pragma unroll
+      for (int g = 0; g < GMAX; ++g) {
+        if (!EXACT && g >= G) continue;
+        float tmax = s[0][g];
+#pragma unroll
+        for (int u = 1; u < UNROLL; ++u) tmax = fmaxf(tmax, s[u][g]);
+        const float mnew = fmaxf(m[g], tmax);
+        const float alpha = (mnew == -INFINITY) ? 1.f : exp2f(m[g] - mnew);
+        m[g] = mnew;
+        lsum[g] *= alpha;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[g][j] *= alpha;
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+          const float p = ok[u] ? exp2f(s[u][g] - mnew) : 0.f;
+          lsum[g] += p;
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) acc[g][j] = fmaf(p, E::load(vp[u].v[j]), acc[g][j]);
+        }
       }
     }
   }
 
-  // Merge the per-row-group partials across the wave.
+  // Merge the PPW lane-group states: rescale to the wave max, then sum.
 #pragma unroll
   for (int g = 0; g < GMAX; ++g) {
-    lsum[g] = xor_sum<LPR, kWave>(lsum[g]);
+    const float mw = xor_max<LPR, kWave>(m[g]);
+    const float f = (m[g] == -INFINITY) ? 0.f : exp2f(m[g] - mw);
+    m[g] = mw;
+    lsum[g] = xor_sum<LPR, kWave>(lsum[g] * f);
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) acc[g][j] = xor_sum<LPR, kWave>(acc[g][j]);
+    for (int j = 0; j < VEC; ++j) acc[g][j] = xor_sum<LPR, kWave>(acc[g][j] * f);
   }
 
   if (nparts == 1) {
