@@ -89,11 +89,19 @@ int32_t mi_kv_append(const void* keys, int64_t key_token_stride, int64_t key_hea
  * One work item = (sequence, KV head, context partition); all G query heads of
  * the KV head share it, so each K/V row is read from HBM once. split_k = 0
  * picks partitions on the device from context_lens (graph-replay safe);
- * split_k > 0 forces at most split_k partitions per sequence. Sequences with
- * more than one partition are merged by a second, reduce launch.
+ * split_k > 0 forces at most split_k partitions per sequence. Partitions
+ * of one (sequence, KV head) are merged inside the same launch: each
+ * publishes its online-softmax state to `workspace` and bumps an arrival
+ * counter; the last arrival merges all of them and writes the output.
  *
  * workspace: float32 device buffer of at least
- * mi_paged_decode_workspace_bytes(...) bytes (may be NULL when that is 0).
+ * mi_paged_decode_workspace_bytes(...) bytes, 256-byte aligned (may be NULL
+ * when that is 0); no initialisation needed.
+ * counters: int32 device array of at least num_seqs * num_kv_heads entries
+ * that must be ZERO on entry; every call leaves it zero again, so one array
+ * can serve all later calls on the same stream. Calls that run concurrently
+ * (different streams) need separate counters and workspaces. May be NULL
+ * when the workspace size is 0.
  * Sequences with context_len 0 produce zeros.
  */
 int64_t mi_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
@@ -102,10 +110,10 @@ int64_t mi_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
 
 /*
  * Tuning of the adaptive partition plan (split_k = 0): aim for about
- * target_items (work item, KV head) wavefronts per launch, each covering at
+ * target_items (work item, KV head) workgroups per launch, each covering at
  * least min_part_blocks cache blocks. Values <= 0 leave a knob unchanged.
  * Process-wide; changes the size mi_paged_decode_workspace_bytes reports, so
- * set it before sizing workspaces or capturing graphs. Defaults 2048 / 2.
+ * set it before sizing workspaces or capturing graphs. Defaults 512 / 4.
  */
 void mi_tune_decode(int32_t target_items, int32_t min_part_blocks);
 
@@ -116,7 +124,8 @@ int32_t mi_paged_decode(const void* query, int64_t q_token_stride, int64_t q_hea
                         int64_t block_table_stride, int32_t block_table_width,
                         const int32_t* context_lens, void* out, int64_t out_token_stride,
                         int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
-                        int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                        int32_t* counters, int32_t num_seqs, int32_t num_q_heads,
+                        int32_t num_kv_heads,
                         int32_t head_dim, int32_t block_size, int32_t num_blocks,
                         int32_t split_k, float scale, int32_t dtype, void* stream);
 

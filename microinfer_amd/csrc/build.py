@@ -38,30 +38,34 @@ COMMON_FLAGS = [
 ]
 
 
-def _compile(source: Path) -> Path:
-    obj = BUILD_DIR / (source.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(source), "-o", str(obj)]
+def _compile(source: Path, build_dir: Path, extra_flags: tuple[str, ...]) -> Path:
+    obj = build_dir / (source.stem + ".o")
+    cmd = [HIPCC, *COMMON_FLAGS, *extra_flags, "-c", str(source), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {source.name}:\n{proc.stderr}")
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+def build(verbose: bool = False, *, extra_flags: tuple[str, ...] = (),
+          output: Path | None = None) -> Path:
+    """Compile and link; ``extra_flags``/``output`` build a variant library."""
+    library = LIBRARY if output is None else Path(output)
+    build_dir = BUILD_DIR if output is None else library.parent / (library.stem + "_build")
+    build_dir.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     workers = min(len(sources), max(1, min(16, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(workers) as pool:
-        objects = list(pool.map(_compile, sources))
-    tmp = LIBRARY.with_suffix(".so.tmp")
+        objects = list(pool.map(lambda s: _compile(s, build_dir, tuple(extra_flags)), sources))
+    tmp = library.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *map(str, objects)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
-    os.replace(tmp, LIBRARY)
+    os.replace(tmp, library)
     if verbose:
-        print(f"built {LIBRARY} from {len(sources)} sources", file=sys.stderr)
-    return LIBRARY
+        print(f"built {library} from {len(sources)} sources", file=sys.stderr)
+    return library
 
 
 if __name__ == "__main__":

@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include <string>
+#include <type_traits>
 
 #include "mi_attn.h"
 
@@ -23,10 +24,18 @@ struct F32 {
   static __device__ __forceinline__ raw store(float x) { return x; }
 };
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
 struct BF16 {
   using raw = uint16_t;
   static __device__ __forceinline__ float load(raw x) {
     return __uint_as_float(static_cast<uint32_t>(x) << 16);
+  }
+  // a.lo*b.lo + a.hi*b.hi + c on two packed elements (v_dot2_f32_bf16).
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                          __builtin_bit_cast(bf16x2_t, b), c, false);
   }
   // Round to nearest even; NaN becomes the canonical quiet NaN 0x7FC0.
   static __device__ __forceinline__ raw store(float f) {
@@ -41,6 +50,11 @@ struct F16 {
   using raw = uint16_t;
   static __device__ __forceinline__ float load(raw x) {
     return static_cast<float>(__builtin_bit_cast(_Float16, x));
+  }
+  // a.lo*b.lo + a.hi*b.hi + c on two packed elements (v_dot2_f32_f16).
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b),
+                                  c, false);
   }
   static __device__ __forceinline__ raw store(float f) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
@@ -69,6 +83,29 @@ __device__ __forceinline__ Pack<R, N> zero_pack() {
 #pragma unroll
   for (int i = 0; i < N; ++i) z.v[i] = R(0);
   return z;
+}
+
+// ---------------------------------------------------------------------------
+// Cross-workgroup hand-off without whole-cache maintenance. Relaxed
+// agent-scope atomic loads and stores compile to global_load/store with the
+// sc1 bit, which is coherent across the per-XCD L2 caches; a release fence
+// would instead write back and invalidate the entire L2 of every writer.
+// A writer publishes with store_coherent, waits for its stores to complete
+// (wait_stores), then signals with an agent-scope atomic; a reader that
+// observed the signal reads with load_coherent.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void wait_stores() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 // ---------------------------------------------------------------------------

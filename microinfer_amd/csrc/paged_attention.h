@@ -23,6 +23,7 @@ struct AttnArgs {
   int64_t o_ts, o_hs;
   float* ws_acc;  // split partials: [items, Hkv, G, D] unnormalised sums
   float* ws_ml;   // split partials: [items, Hkv, G, 2] (log2-domain max, sum)
+  int32_t* counters;  // [num_seqs * Hkv] arrival counts; zero on entry and exit
   int32_t num_seqs;  // decode: sequences; varlen: requests
   int32_t num_rows;  // varlen: query rows
   int32_t num_kv_heads, group, head_dim, block_size, log2_block, num_blocks;

@@ -11,10 +11,11 @@ int32_t launch_vector_bf16(const AttnArgs& a, hipStream_t stream);
 
 namespace {
 
-// Adaptive split-K tuning: the decode launch aims for about kTargetItems
-// (work item, KV head) wavefronts, each covering at least kMinPartBlocks blocks.
-int32_t g_target_items = 2048;
-int32_t g_min_part_blocks = 2;
+// Adaptive split-K tuning: the decode launch aims for about g_target_items
+// (work item, KV head) workgroups, each covering at least g_min_part_blocks
+// blocks.
+int32_t g_target_items = 512;
+int32_t g_min_part_blocks = 4;
 
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -81,7 +82,8 @@ extern "C" int32_t mi_paged_decode(
     int64_t cache_head_stride, const int32_t* block_tables, int64_t block_table_stride,
     int32_t block_table_width, const int32_t* context_lens, void* out,
     int64_t out_token_stride, int64_t out_head_stride, void* workspace,
-    int64_t workspace_bytes, int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+    int64_t workspace_bytes, int32_t* counters, int32_t num_seqs, int32_t num_q_heads,
+    int32_t num_kv_heads,
     int32_t head_dim, int32_t block_size, int32_t num_blocks, int32_t split_k, float scale,
     int32_t dtype, void* stream) {
   using namespace mi;
@@ -107,6 +109,8 @@ extern "C" int32_t mi_paged_decode(
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 256)))
     return fail(MI_ERR_WORKSPACE, "mi_paged_decode: workspace needs " +
                                       std::to_string(need) + " bytes (256-byte aligned)");
+  if (need > 0 && counters == nullptr)
+    return fail(MI_ERR_WORKSPACE, "mi_paged_decode: split partitions need zeroed counters");
 
   AttnArgs a{};
   a.q = query;
@@ -142,6 +146,7 @@ extern "C" int32_t mi_paged_decode(
         static_cast<int64_t>(a.max_items) * num_kv_heads * a.group * head_dim;
     a.ws_acc = static_cast<float*>(workspace);
     a.ws_ml = a.ws_acc + acc_floats;
+    a.counters = counters;
   }
   return dispatch_vector(a, dtype, static_cast<hipStream_t>(stream));
 }

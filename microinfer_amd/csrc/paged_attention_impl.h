@@ -1,6 +1,6 @@
-// Vector (non-MFMA) paged attention kernels for gfx950.
+// Vector (non-MFMA) paged attention kernel for gfx950.
 //
-// Decode replaces _paged_decode_kernel / _paged_decode_reduce_kernel
+// Decode replaces _paged_decode_kernel + _paged_decode_reduce_kernel
 // (microinfer/layer/triton_paged_attention.py:40-131, :236-257); varlen mode
 // covers causal prefill rows for dtypes or shapes the MFMA kernel does not
 // take, replacing the reference-path fallback (layer/paged_attention.py:22-67).
@@ -10,15 +10,20 @@
 //    All G = Hq/Hkv query heads of that KV head are processed together, so a
 //    K/V row is fetched from HBM once per step instead of G times.
 //  * A head row of D elements is spread over LPR lanes, VEC elements (16 B)
-//    per lane, so one load instruction fetches PPW = 64/LPR whole rows; a tile
-//    issues UNROLL such K loads and UNROLL V loads before any arithmetic.
-//  * Scores: per-lane partial dot products, xor-reduced over the LPR lanes of
-//    a row. Online softmax runs in the log2 domain (q is pre-scaled by
-//    scale*log2 e) with a wave-uniform running max, so the running sum and the
-//    P.V accumulator stay per-lane partials until one final cross-lane merge.
+//    per lane, so one load instruction fetches PPW = 64/LPR whole rows. A tile
+//    is UNROLL such K loads plus UNROLL V loads, and tiles are double-buffered
+//    in registers: tile i+1 is in flight while tile i is computed.
+//  * Scores: per-lane partial dot products summed over the LPR lanes of a row
+//    with DPP. Each lane group (PPW of them per wave) keeps its own
+//    online-softmax state in the log2 domain (q is pre-scaled by scale*log2 e);
+//    the groups are merged once at the end.
 //  * Partitions are planned on the device from context_lens: every wave
 //    recomputes the same prefix sum over sequences, so the launch shape
 //    depends only on the batch size and stays valid under hipGraph replay.
+//  * Partitions of one (sequence, KV head) are merged in the same launch: each
+//    publishes (acc, m, l) with L2-coherent stores and bumps an arrival
+//    counter; the last arrival merges and writes the output, then re-zeroes
+//    the counter.
 #pragma once
 
 #include "paged_attention.h"
@@ -34,10 +39,8 @@ struct WorkItem {
 //  PB    = adaptive: max(min_part_blocks, ceil(sum nb * Hkv / target_items))
 //          forced:   ceil(nb_r / min(split_k, nb_r)) per sequence
 //  parts_r = max(1, ceil(nb_r / PB)); items are numbered sequence-major.
-// Finds the item with index `key` (by_seq = false) or the first item of
-// sequence `key` (by_seq = true). Returns false when no such item exists.
-__device__ __forceinline__ bool decode_plan(const AttnArgs& a, int key, bool by_seq, int lane,
-                                            WorkItem& it) {
+// Finds work item `key`; returns false when the launch has fewer items.
+__device__ __forceinline__ bool decode_plan(const AttnArgs& a, int key, int lane, WorkItem& it) {
   const int B = a.block_size;
   const int lb = a.log2_block;
   const int max_ctx = a.t_width * B;
@@ -73,8 +76,7 @@ __device__ __forceinline__ bool decode_plan(const AttnArgs& a, int key, bool by_
     }
     const int incl = wave_inclusive_scan(np, lane);
     const int start = running + incl - np;
-    const bool mine = (r < a.num_seqs) &&
-                      (by_seq ? (r == key) : (key >= start && key < start + np));
+    const bool mine = (r < a.num_seqs) && key >= start && key < start + np;
     const uint64_t hit = __ballot(mine);
     if (hit) {
       const int src = __ffsll(static_cast<unsigned long long>(hit)) - 1;
@@ -84,9 +86,8 @@ __device__ __forceinline__ bool decode_plan(const AttnArgs& a, int key, bool by_
       it.seq = __shfl(r, src, kWave);
       it.nparts = __shfl(np, src, kWave);
       it.ctx = __shfl(c, src, kWave);
-      it.part = by_seq ? first : key - first;  // by_seq: first item index
-      const int p = by_seq ? 0 : it.part;
-      it.blk_begin = p * pbs;
+      it.part = key - first;
+      it.blk_begin = it.part * pbs;
       it.blk_end = min(nbs, it.blk_begin + pbs);
       return true;
     }
@@ -95,12 +96,23 @@ __device__ __forceinline__ bool decode_plan(const AttnArgs& a, int key, bool by_
   return false;
 }
 
-template <typename E, int VEC, int LPR, int GMAX, bool EXACT, int UNROLL>
-__global__ __launch_bounds__(kWave) void paged_attention_vector_kernel(const AttnArgs a) {
+// One double-buffer slot: UNROLL K and V packs plus a validity bit per load.
+template <typename R, int VEC, int UNROLL>
+struct KVTile {
+  Pack<R, VEC> k[UNROLL];
+  Pack<R, VEC> v[UNROLL];
+  uint32_t ok;
+};
+
+template <typename E, int VEC, int LPR, int GMAX, bool EXACT, int UNROLL, bool FAST, int NW>
+__global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(const AttnArgs a) {
   using R = typename E::raw;
+  using Tile = KVTile<R, VEC, UNROLL>;
+  constexpr int D = VEC * LPR;
   constexpr int PPW = kWave / LPR;  // rows per load instruction
   constexpr int TILE = PPW * UNROLL;
-  const int lane = threadIdx.x;
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
   const int grp = lane / LPR;
   const int sub = lane % LPR;
   const int d0 = sub * VEC;
@@ -108,7 +120,8 @@ __global__ __launch_bounds__(kWave) void paged_attention_vector_kernel(const Att
   const int w = blockIdx.x;
   const int G = EXACT ? GMAX : a.group;
 
-  int seq, q_row, ctx, blk_begin, blk_end, nparts;
+  // Every wave derives the same work item, so no barrier is needed here.
+  int seq, q_row, ctx, blk_begin, blk_end, nparts, first_item = 0;
   if (a.varlen) {
     q_row = w;
     int lo = 0, hi = a.num_seqs - 1;
@@ -127,7 +140,7 @@ __global__ __launch_bounds__(kWave) void paged_attention_vector_kernel(const Att
     nparts = 1;
   } else {
     WorkItem it;
-    if (!decode_plan(a, w, false, lane, it)) return;
+    if (!decode_plan(a, w, lane, it)) return;  // uniform across the workgroup
     // The plan is identical on every lane; keep it in scalar registers.
     seq = __builtin_amdgcn_readfirstlane(it.seq);
     q_row = seq;
@@ -135,22 +148,26 @@ __global__ __launch_bounds__(kWave) void paged_attention_vector_kernel(const Att
     blk_begin = __builtin_amdgcn_readfirstlane(it.blk_begin);
     blk_end = __builtin_amdgcn_readfirstlane(it.blk_end);
     nparts = __builtin_amdgcn_readfirstlane(it.nparts);
+    first_item = w - __builtin_amdgcn_readfirstlane(it.part);
   }
 
-  // Query rows of the G heads, pre-scaled into the log2 domain.
+  // Query rows of the G heads. 16-bit types keep raw element pairs for the
+  // packed dot2 instructions; scores are scaled into the log2 domain after
+  // the row sum.
+  constexpr bool PAIRS = sizeof(R) == 2;
+  constexpr int QW = PAIRS ? VEC / 2 : VEC;
+  using QWord = typename std::conditional<PAIRS, uint32_t, float>::type;
   const R* qbase = static_cast<const R*>(a.q) + q_row * a.q_ts + d0;
-  float qf[GMAX][VEC];
+  QWord qv[GMAX][QW];
 #pragma unroll
   for (int g = 0; g < GMAX; ++g) {
-    if (EXACT || g < G) {
-      const Pack<R, VEC> qp = load_pack<R, VEC>(qbase + (head * G + g) * a.q_hs);
+    Pack<R, VEC> qp = zero_pack<R, VEC>();
+    if (EXACT || g < G) qp = load_pack<R, VEC>(qbase + (head * G + g) * a.q_hs);
+    const Pack<QWord, QW> words = __builtin_bit_cast(Pack<QWord, QW>, qp);
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) qf[g][j] = E::load(qp.v[j]) * a.scale_log2;
-    } else {
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) qf[g][j] = 0.f;
-    }
+    for (int j = 0; j < QW; ++j) qv[g][j] = words.v[j];
   }
+  const float scale_log2 = a.scale_log2;
 
   float m[GMAX], lsum[GMAX], acc[GMAX][VEC];
 #pragma unroll
@@ -163,17 +180,19 @@ __global__ __launch_bounds__(kWave) void paged_attention_vector_kernel(const Att
 
   const R* kc = static_cast<const R*>(a.kc);
   const R* vc = static_cast<const R*>(a.vc);
-  // Contiguous mode (varlen only, no block table): request `seq` owns K/V rows
-  // cu_k[seq] .. cu_k[seq + 1] - 1 of a [rows, Hkv, D] array; num_blocks holds
-  // the row count. It runs as one "block" that spans the whole request.
-  const bool paged = a.tables != nullptr;
+  // Contiguous mode (general path, varlen only, no block table): request `seq`
+  // owns K/V rows cu_k[seq] .. cu_k[seq + 1] - 1 of a [rows, Hkv, D] array;
+  // num_blocks holds the row count. It runs as one "block" spanning the request.
+  const bool paged = FAST || a.tables != nullptr;
   const int32_t* trow = paged ? a.tables + seq * a.t_stride : nullptr;
   const int64_t row0 = paged ? 0 : a.cu_k[seq];
   const int lb = paged ? a.log2_block : 30;
   const int bmask = paged ? a.block_size - 1 : (1 << 30) - 1;
-  const int64_t base_off = head * a.c_hs + d0 + row0 * a.c_ts;
-  // Any in-bounds address; masked rows load from here and are discarded.
-  const int64_t safe_off = head * a.c_hs + d0;
+  // Scalar part of a row address (block, row-in-block, head) + per-lane part
+  // (row within the load group, column). Masked loads read row 0 of block 0.
+  const int64_t head_off = head * a.c_hs + row0 * a.c_ts;
+  const int64_t safe_head_off = head * a.c_hs;
+  const int lane_off = grp * static_cast<int>(a.c_ts) + d0;
   int pos_begin, pos_end;
   if (paged) {
     pos_begin = blk_begin << lb;
@@ -183,95 +202,118 @@ __global__ __launch_bounds__(kWave) void paged_attention_vector_kernel(const Att
     pos_end = static_cast<int>(min<int64_t>(ctx, max<int64_t>(a.num_blocks - row0, 0)));
     blk_end = 1;
   }
-  // A load instruction covers PPW consecutive positions; when PPW <= B they
-  // always share one block, so its id is wave-uniform and read with readlane.
-  const bool uniform_ids = !paged || PPW <= a.block_size;
+  const int last_blk = paged ? max(blk_end - 1, 0) : 0;
+  // Fast path (host guarantees a table and PPW <= B): the PPW positions of a
+  // load share one block, so its id is wave-uniform. Ids are fetched with
+  // scalar loads (constant address space), which keeps the lookups off the
+  // vector-memory counter that orders the in-flight K/V loads.
+  using ConstI32 = __attribute__((address_space(4))) const int32_t;
+  ConstI32* ctab = (ConstI32*)(trow);  // address-space conversion needs a C cast
 
-  // Block ids of up to 64 blocks live in registers (one per lane).
-  for (int chunk = blk_begin; chunk < blk_end; chunk += kWave) {
-    const int cpos_begin = paged ? max(pos_begin, chunk << lb) : pos_begin;
-    const int cpos_end = paged ? min(pos_end, (chunk + kWave) << lb) : pos_end;
-    if (cpos_begin >= cpos_end) break;
-    int my_blk = 0;
-    if (paged) {
-      const int b = chunk + lane;
-      my_blk = b < blk_end ? trow[b] : -1;
-    }
-
-    for (int t0 = cpos_begin; t0 < cpos_end; t0 += TILE) {
-      int64_t off[UNROLL];
-      bool ok[UNROLL];
-      if (uniform_ids) {
-        // Block address is scalar; each lane adds its row and column.
-        const int64_t lane_off = grp * a.c_ts + base_off;
+  // Issue the K/V loads of the tile starting at t0 into slot T.
+  auto issue = [&](Tile& T, int t0) {
+    T.ok = 0;
+    if constexpr (FAST) {
+      int ids[UNROLL];  // all scalar id loads first, one wait, then the K/V loads
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-          const int p0 = t0 + u * PPW;
-          const int blk = __builtin_amdgcn_readlane(my_blk, ((p0 >> lb) - chunk) & (kWave - 1));
-          const bool blk_ok = blk >= 0 && blk < a.num_blocks;
-          const int64_t block_off = blk * a.c_bs + (p0 & bmask) * a.c_ts;
-          ok[u] = blk_ok && p0 + grp < cpos_end;
-          off[u] = ok[u] ? block_off + lane_off : safe_off;
-        }
-      } else {
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-          const int pos = t0 + u * PPW + grp;
-          const int blk = __shfl(my_blk, ((pos >> lb) - chunk) & (kWave - 1), kWave);
-          ok[u] = pos < cpos_end && blk >= 0 && blk < a.num_blocks;
-          off[u] = ok[u] ? blk * a.c_bs + (pos & bmask) * a.c_ts + base_off : safe_off;
-        }
-      }
-      // Issue every K and V load of the tile before any arithmetic.
-      Pack<R, VEC> kp[UNROLL], vp[UNROLL];
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u) kp[u] = load_pack<R, VEC>(kc + off[u]);
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u) vp[u] = load_pack<R, VEC>(vc + off[u]);
-
-      // Scores of this lane group's UNROLL positions.
-      float s[UNROLL][GMAX];
+      for (int u = 0; u < UNROLL; ++u) ids[u] = ctab[min((t0 + u * PPW) >> lb, last_blk)];
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) {
-        float kf[VEC];
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) kf[j] = E::load(kp[u].v[j]);
-#pragma unroll
-        for (int g = 0; g < GMAX; ++g) {
-          float dot = 0.f;
-#pragma unroll
-          for (int j = 0; j < VEC; ++j) dot = fmaf(qf[g][j], kf[j], dot);
-          dot = group_sum<LPR>(dot);
-          s[u][g] = ok[u] ? dot : -INFINITY;
-        }
+        const int p0 = t0 + u * PPW;
+        const int blk = ids[u];
+        const bool blk_ok = p0 < pos_end && blk >= 0 && blk < a.num_blocks;
+        const bool lane_ok = blk_ok && p0 + grp < pos_end;
+        const int64_t soff = blk_ok ? blk * a.c_bs + (p0 & bmask) * a.c_ts + head_off
+                                    : safe_head_off;
+        const int loff = lane_ok ? lane_off : d0;
+        T.k[u] = load_pack<R, VEC>(kc + soff + loff);
+        T.v[u] = load_pack<R, VEC>(vc + soff + loff);
+        T.ok |= static_cast<uint32_t>(lane_ok) << u;
       }
+    } else {
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const int pos = t0 + u * PPW + grp;
+        const int blk = paged ? trow[min(pos >> lb, last_blk)] : 0;
+        const bool ok = pos < pos_end && blk >= 0 && blk < a.num_blocks;
+        const int64_t off = ok ? blk * a.c_bs + (pos & bmask) * a.c_ts + head_off + d0
+                               : safe_head_off + d0;
+        T.k[u] = load_pack<R, VEC>(kc + off);
+        T.v[u] = load_pack<R, VEC>(vc + off);
+        T.ok |= static_cast<uint32_t>(ok) << u;
+      }
+    }
+  };
 
-      // Online softmax per lane group (each group is its own split; groups
-      // are merged once at the end), then P.V.
+  // Online softmax + P.V over one loaded tile (this lane group's positions).
+  auto consume = [&](const Tile& T) {
+    float s[UNROLL][GMAX];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const Pack<QWord, QW> kw = __builtin_bit_cast(Pack<QWord, QW>, T.k[u]);
+      const bool ok = (T.ok >> u) & 1u;
 #pragma unroll
       for (int g = 0; g < GMAX; ++g) {
-        if (!EXACT && g >= G) continue;
-        float tmax = s[0][g];
+        float dot = 0.f;
 #pragma unroll
-        for (int u = 1; u < UNROLL; ++u) tmax = fmaxf(tmax, s[u][g]);
-        const float mnew = fmaxf(m[g], tmax);
-        const float alpha = (mnew == -INFINITY) ? 1.f : exp2f(m[g] - mnew);
-        m[g] = mnew;
-        lsum[g] *= alpha;
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) acc[g][j] *= alpha;
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-          const float p = ok[u] ? exp2f(s[u][g] - mnew) : 0.f;
-          lsum[g] += p;
-#pragma unroll
-          for (int j = 0; j < VEC; ++j) acc[g][j] = fmaf(p, E::load(vp[u].v[j]), acc[g][j]);
+        for (int j = 0; j < QW; ++j) {
+          if constexpr (PAIRS) {
+            dot = E::dot2(qv[g][j], kw.v[j], dot);
+          } else {
+            dot = fmaf(qv[g][j], kw.v[j], dot);
+          }
         }
+        dot = group_sum<LPR>(dot) * scale_log2;
+        s[u][g] = ok ? dot : -INFINITY;
       }
+    }
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      if (!EXACT && g >= G) continue;
+      float tmax = s[0][g];
+#pragma unroll
+      for (int u = 1; u < UNROLL; ++u) tmax = fmaxf(tmax, s[u][g]);
+      const float mnew = fmaxf(m[g], tmax);
+      const float alpha = (mnew == -INFINITY) ? 1.f : exp2f(m[g] - mnew);
+      m[g] = mnew;
+      lsum[g] *= alpha;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) acc[g][j] *= alpha;
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const float p = ((T.ok >> u) & 1u) ? exp2f(s[u][g] - mnew) : 0.f;
+        lsum[g] += p;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[g][j] = fmaf(p, E::load(T.v[u].v[j]), acc[g][j]);
+      }
+    }
+  };
+
+  // Double-buffered tile loop. The NW waves interleave the partition's tiles
+  // (wave k takes tiles k, k + NW, ...); tile i+1 is in flight while tile i is
+  // used.
+  constexpr int STRIDE = TILE * NW;
+  if (pos_begin + wave * TILE < pos_end) {
+    Tile A, B;
+    int t0 = pos_begin + wave * TILE;
+    issue(A, t0);
+    while (true) {
+      const int t1 = t0 + STRIDE;
+      const bool more = t1 < pos_end;
+      if (more) issue(B, t1);
+      consume(A);
+      if (!more) break;
+      const int t2 = t1 + STRIDE;
+      const bool more2 = t2 < pos_end;
+      if (more2) issue(A, t2);
+      consume(B);
+      if (!more2) break;
+      t0 = t2;
     }
   }
 
-  // Merge the PPW lane-group states: rescale to the wave max, then sum.
+  // Merge the PPW lane-group states of this wave: rescale to the wave max,
+  // then sum across groups.
 #pragma unroll
   for (int g = 0; g < GMAX; ++g) {
     const float mw = xor_max<LPR, kWave>(m[g]);
@@ -282,9 +324,51 @@ __global__ __launch_bounds__(kWave) void paged_attention_vector_kernel(const Att
     for (int j = 0; j < VEC; ++j) acc[g][j] = xor_sum<LPR, kWave>(acc[g][j] * f);
   }
 
+  // Merge the NW wave states through LDS; wave 0 carries on alone.
+  if constexpr (NW > 1) {
+    __shared__ float s_acc[NW][GMAX][D];
+    __shared__ float s_ml[NW][GMAX][2];
+    if (grp == 0) {
+#pragma unroll
+      for (int g = 0; g < GMAX; ++g)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) s_acc[wave][g][d0 + j] = acc[g][j];
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int g = 0; g < GMAX; ++g) {
+        s_ml[wave][g][0] = m[g];
+        s_ml[wave][g][1] = lsum[g];
+      }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      float mx = s_ml[0][g][0];
+#pragma unroll
+      for (int k = 1; k < NW; ++k) mx = fmaxf(mx, s_ml[k][g][0]);
+      float l = 0.f, o[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) o[j] = 0.f;
+#pragma unroll
+      for (int k = 0; k < NW; ++k) {
+        const float mk = s_ml[k][g][0];
+        const float f = (mk == -INFINITY) ? 0.f : exp2f(mk - mx);
+        l = fmaf(f, s_ml[k][g][1], l);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) o[j] = fmaf(f, s_acc[k][g][d0 + j], o[j]);
+      }
+      m[g] = mx;
+      lsum[g] = l;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) acc[g][j] = o[j];
+    }
+  }
+
+  R* obase = static_cast<R*>(a.out) + q_row * a.o_ts + d0;
   if (nparts == 1) {
     if (grp == 0) {
-      R* obase = static_cast<R*>(a.out) + q_row * a.o_ts + d0;
 #pragma unroll
       for (int g = 0; g < GMAX; ++g) {
         if (!EXACT && g >= G) continue;
@@ -295,68 +379,139 @@ __global__ __launch_bounds__(kWave) void paged_attention_vector_kernel(const Att
         store_pack<R, VEC>(obase + (head * G + g) * a.o_hs, o);
       }
     }
-  } else {
+    return;
+  }
+
+  // Publish this partition's state, then count arrivals; the last workgroup
+  // of the (sequence, KV head) merges every partition and writes the output.
+  // Partials of item w: ws_acc[(w*Hkv + head)*G + g][D], ws_ml[...][2].
+  {
+    const int64_t base = (static_cast<int64_t>(w) * a.num_kv_heads + head) * G;
 #pragma unroll
     for (int g = 0; g < GMAX; ++g) {
       if (!EXACT && g >= G) continue;
-      const int64_t idx = (static_cast<int64_t>(w) * a.num_kv_heads + head) * G + g;
       if (grp == 0) {
-        Pack<float, VEC> o;
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) o.v[j] = acc[g][j];
-        store_pack<float, VEC>(a.ws_acc + idx * a.head_dim + d0, o);
+        for (int j = 0; j < VEC; ++j)
+          store_coherent(a.ws_acc + (base + g) * D + d0 + j, acc[g][j]);
       }
       if (lane == 0) {
-        a.ws_ml[idx * 2] = m[g];
-        a.ws_ml[idx * 2 + 1] = lsum[g];
+        store_coherent(a.ws_ml + (base + g) * 2, m[g]);
+        store_coherent(a.ws_ml + (base + g) * 2 + 1, lsum[g]);
       }
     }
   }
+  wait_stores();  // partials have reached the coherent level before arrival
+  int32_t* counter = a.counters + static_cast<int64_t>(seq) * a.num_kv_heads + head;
+  int arrived = 0;
+  if (lane == 0)
+    arrived = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  arrived = __shfl(arrived, 0, kWave);
+  if (arrived != nparts - 1) return;
+
+  // Last arrival: out = sum_i 2^(m_i - M) acc_i / sum_i 2^(m_i - M) l_i,
+  // M = max_i m_i (the merge of microinfer/layer/triton_paged_attention.py:
+  // 244-257 in the log2 domain; empty partitions, m = -inf, weigh zero).
+  auto item_row = [&](int part, int g) {
+    return (static_cast<int64_t>(first_item + part) * a.num_kv_heads + head) * G + g;
+  };
+  // Pass 1: lane i reads partition i's maxima.
+  float mx[GMAX];
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) mx[g] = -INFINITY;
+  for (int i = lane; i < nparts; i += kWave) {
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g)
+      if (EXACT || g < G) mx[g] = fmaxf(mx[g], load_coherent(a.ws_ml + item_row(i, g) * 2));
+  }
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) mx[g] = xor_max<1, kWave>(mx[g]);
+
+  // Pass 2, per batch of 64 partitions: weights on lane i; lane group grp
+  // then sums partitions grp, grp + PPW, ... of the batch for its columns,
+  // DEPTH partitions at a time with all their loads issued before use.
+  constexpr int DEPTH = (GMAX * VEC >= 64) ? 1 : 64 / (GMAX * VEC);
+  float total[GMAX], num[GMAX][VEC];
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) {
+    total[g] = 0.f;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) num[g][j] = 0.f;
+  }
+  for (int base = 0; base < nparts; base += kWave) {
+    const int i = base + lane;
+    float wgt[GMAX];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      wgt[g] = 0.f;
+      if ((EXACT || g < G) && i < nparts) {
+        const float mi = load_coherent(a.ws_ml + item_row(i, g) * 2);
+        const float li = load_coherent(a.ws_ml + item_row(i, g) * 2 + 1);
+        wgt[g] = (mi == -INFINITY) ? 0.f : exp2f(mi - mx[g]);
+        total[g] = fmaf(wgt[g], li, total[g]);
+      }
+    }
+    const int batch = min(kWave, nparts - base);
+    for (int k0 = 0; k0 * PPW < batch; k0 += DEPTH) {
+      float vals[DEPTH][GMAX][VEC];
+      float wj[DEPTH][GMAX];
+#pragma unroll
+      for (int kk = 0; kk < DEPTH; ++kk) {
+        const int j0 = grp + (k0 + kk) * PPW;
+        const bool valid = j0 < batch;
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+          wj[kk][g] = __shfl(wgt[g], j0 & (kWave - 1), kWave);
+          const float* src = a.ws_acc + item_row(base + (valid ? j0 : 0), g) * D + d0;
+#pragma unroll
+          for (int j = 0; j < VEC; ++j)
+            vals[kk][g][j] = ((EXACT || g < G) && valid) ? load_coherent(src + j) : 0.f;
+          if (!valid) wj[kk][g] = 0.f;
+        }
+      }
+#pragma unroll
+      for (int kk = 0; kk < DEPTH; ++kk)
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g)
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) num[g][j] = fmaf(wj[kk][g], vals[kk][g][j], num[g][j]);
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) {
+    if (!EXACT && g >= G) continue;
+    const float t = xor_sum<1, kWave>(total[g]);
+    float out[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) out[j] = xor_sum<LPR, kWave>(num[g][j]);
+    if (grp == 0) {
+      const float inv = t > 0.f ? 1.f / t : 0.f;
+      Pack<R, VEC> o;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) o.v[j] = E::store(out[j] * inv);
+      store_pack<R, VEC>(obase + (head * G + g) * a.o_hs, o);
+    }
+  }
+  // Leave the counter zeroed for the next launch (all partitions arrived).
+  if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Merge the partition partials of each (sequence, KV head):
-//   out = sum_i 2^(m_i - M) acc_i / sum_i 2^(m_i - M) l_i,  M = max_i m_i
-// (the merge of microinfer/layer/triton_paged_attention.py:244-257, in the log2
-// domain). Empty partitions (m = -inf) weigh zero.
-template <typename E>
-__global__ __launch_bounds__(kWave) void paged_decode_reduce_kernel(const AttnArgs a) {
-  using R = typename E::raw;
-  const int lane = threadIdx.x;
-  const int head = blockIdx.y;
-  WorkItem it;
-  if (!decode_plan(a, blockIdx.x, true, lane, it)) return;
-  if (it.nparts <= 1) return;
-  const int first = it.part;
-  const int G = a.group;
-  const int D = a.head_dim;
-  for (int g = 0; g < G; ++g) {
-    float mx = -INFINITY;
-    for (int i = lane; i < it.nparts; i += kWave) {
-      const int64_t idx = (static_cast<int64_t>(first + i) * a.num_kv_heads + head) * G + g;
-      mx = fmaxf(mx, a.ws_ml[idx * 2]);
-    }
-    mx = xor_max<1, kWave>(mx);
-    float total = 0.f;
-    for (int i = lane; i < it.nparts; i += kWave) {
-      const int64_t idx = (static_cast<int64_t>(first + i) * a.num_kv_heads + head) * G + g;
-      const float mi = a.ws_ml[idx * 2];
-      const float wgt = (mi == -INFINITY) ? 0.f : exp2f(mi - mx);
-      total += wgt * a.ws_ml[idx * 2 + 1];
-    }
-    total = xor_sum<1, kWave>(total);
-    const float inv = total > 0.f ? 1.f / total : 0.f;
-    R* obase = static_cast<R*>(a.out) + it.seq * a.o_ts + (head * G + g) * a.o_hs;
-    for (int d = lane; d < D; d += kWave) {
-      float num = 0.f;
-      for (int i = 0; i < it.nparts; ++i) {
-        const int64_t idx = (static_cast<int64_t>(first + i) * a.num_kv_heads + head) * G + g;
-        const float mi = a.ws_ml[idx * 2];
-        const float wgt = (mi == -INFINITY) ? 0.f : exp2f(mi - mx);
-        num = fmaf(wgt, a.ws_acc[idx * D + d], num);
-      }
-      obase[d] = E::store(num * inv);
-    }
-  }
+// Loads per tile (per K and per V). Larger GQA groups hold more accumulator
+// registers, so they use shorter tiles to keep two waves per SIMD resident.
+#ifndef MI_TILE_UNROLL_SMALL_GROUP
+#define MI_TILE_UNROLL_SMALL_GROUP 4
+#endif
+#ifndef MI_TILE_UNROLL_LARGE_GROUP
+#define MI_TILE_UNROLL_LARGE_GROUP 4
+#endif
+#ifndef MI_WAVES_PER_GROUP
+#define MI_WAVES_PER_GROUP 4
+#endif
+// Waves per workgroup: they split one partition and merge through LDS.
+constexpr int kWavesPerGroup = MI_WAVES_PER_GROUP;
+
+constexpr int tile_unroll(int gmax) {
+  return gmax <= 2 ? MI_TILE_UNROLL_SMALL_GROUP : MI_TILE_UNROLL_LARGE_GROUP;
 }
 
 // Dispatch over head_dim and group size for one element type.
@@ -373,7 +528,12 @@ int32_t launch_vector_typed(const AttnArgs& a, hipStream_t stream) {
   do {                                                                                  \
     constexpr int VEC_ = (DIM) < kPackElems ? (DIM) : kPackElems;                       \
     constexpr int LPR_ = (DIM) / VEC_;                                                  \
-    paged_attention_vector_kernel<E, VEC_, LPR_, GM, EX, 8><<<grid, kWave, 0, stream>>>(a); \
+    if (a.tables != nullptr && kWave / LPR_ <= a.block_size)                            \
+      paged_attention_vector_kernel<E, VEC_, LPR_, GM, EX, tile_unroll(GM), true,         \
+                                    kWavesPerGroup><<<grid, kWave * kWavesPerGroup, 0, stream>>>(a); \
+    else                                                                                \
+      paged_attention_vector_kernel<E, VEC_, LPR_, GM, EX, tile_unroll(GM), false,        \
+                                    kWavesPerGroup><<<grid, kWave * kWavesPerGroup, 0, stream>>>(a); \
     launched = true;                                                                    \
   } while (0)
 
@@ -405,14 +565,7 @@ int32_t launch_vector_typed(const AttnArgs& a, hipStream_t stream) {
     return fail(MI_ERR_UNSUPPORTED,
                 "paged attention: no kernel for head_dim=" + std::to_string(D) +
                     " group=" + std::to_string(G));
-  int32_t st = check_launch("paged attention");
-  if (st != MI_OK) return st;
-  if (!a.varlen && a.split_k != 1) {
-    const dim3 rgrid(a.num_seqs, a.num_kv_heads);
-    paged_decode_reduce_kernel<E><<<rgrid, kWave, 0, stream>>>(a);
-    st = check_launch("paged decode reduce");
-  }
-  return st;
+  return check_launch("paged attention");
 }
 
 }  // namespace mi

@@ -61,6 +61,26 @@ def _check_caches(key_cache: torch.Tensor, value_cache: torch.Tensor):
     return key_cache, value_cache
 
 
+# Split-merge arrival counters: one zero-filled int32 array per (device,
+# stream). Every decode launch leaves its counters zero again, so the array is
+# reused by all later calls on that stream (including graph replays). A grown
+# array replaces the old one, which stays alive because captured graphs may
+# still point at it.
+_counters: dict[tuple[int, int], torch.Tensor] = {}
+_retired_counters: list[torch.Tensor] = []
+
+
+def _decode_counters(device: torch.device, stream: int, needed: int) -> torch.Tensor:
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    counters = _counters.get(key)
+    if counters is None or counters.numel() < needed:
+        if counters is not None:
+            _retired_counters.append(counters)
+        counters = torch.zeros(max(needed, 4096), dtype=torch.int32, device=device)
+        _counters[key] = counters
+    return counters
+
+
 def decode_workspace_bytes(num_seqs: int, num_q_heads: int, num_kv_heads: int,
                            head_dim: int, split_k: int | None) -> int:
     return int(
@@ -131,9 +151,11 @@ def hip_paged_decode(
             num_requests, num_q_heads, num_kv_heads, head_dim, split
         )
     )
-    workspace = (
-        torch.empty(ws_bytes, dtype=torch.uint8, device=query.device) if ws_bytes else None
-    )
+    stream = _lib.stream_handle(query.device)
+    workspace = counters = None
+    if ws_bytes:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
+        counters = _decode_counters(query.device, stream, num_requests * num_kv_heads)
     status = lib.mi_paged_decode(
         query.data_ptr(), query.stride(0), query.stride(1),
         key_cache.data_ptr(), value_cache.data_ptr(),
@@ -142,9 +164,9 @@ def hip_paged_decode(
         context_lens.data_ptr(),
         output.data_ptr(), output.stride(0), output.stride(1),
         None if workspace is None else workspace.data_ptr(), ws_bytes,
+        None if counters is None else counters.data_ptr(),
         num_requests, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
-        split, float(scale), _lib.dtype_code(query.dtype),
-        _lib.stream_handle(query.device),
+        split, float(scale), _lib.dtype_code(query.dtype), stream,
     )
     _lib.check(status, "mi_paged_decode")
     return output

@@ -41,10 +41,10 @@ def test_invalid_arguments_fail_before_launch():
                               1, 1, 8, 16, 4, 9, None)
     assert status == 1 and "dtype" in _lib.last_error()
     status = lib.mi_paged_decode(None, 0, 0, None, None, 0, 0, 0, None, 0, 1, None, None, 0, 0,
-                                 None, 0, 1, 3, 2, 128, 16, 4, 0, 1.0, 2, None)
+                                 None, 0, None, 1, 3, 2, 128, 16, 4, 0, 1.0, 2, None)
     assert status == 1 and "multiple" in _lib.last_error()
     status = lib.mi_paged_decode(None, 0, 0, None, None, 0, 0, 0, None, 0, 1, None, None, 0, 0,
-                                 None, 0, 1, 4, 2, 96, 16, 4, 0, 1.0, 2, None)
+                                 None, 0, None, 1, 4, 2, 96, 16, 4, 0, 1.0, 2, None)
     assert status == 2 and "head_dim" in _lib.last_error()
     status = lib.mi_paged_prefill(None, 0, 0, None, None, 0, 0, 0, None, None, None, 0, 1,
                                   None, 0, 0, 4, 1, 4, 4, 2, 128, 12, 4, 1.0, 2, None)
@@ -59,7 +59,7 @@ def test_empty_work_is_a_no_op():
     assert lib.mi_kv_append(None, 0, 0, None, 0, 0, None, None, 0, 0, 0, None, None, 0,
                             0, 8, 128, 16, 4, 2, None) == 0
     assert lib.mi_paged_decode(None, 0, 0, None, None, 0, 0, 0, None, 0, 1, None, None, 0, 0,
-                               None, 0, 0, 16, 8, 128, 16, 4, 0, 1.0, 2, None) == 0
+                               None, 0, None, 0, 16, 8, 128, 16, 4, 0, 1.0, 2, None) == 0
 
 
 def test_missing_workspace_is_reported():
@@ -68,9 +68,13 @@ def test_missing_workspace_is_reported():
     assert need > 0
     fake = ctypes.c_void_p(256)
     status = lib.mi_paged_decode(fake, 2048, 128, fake, fake, 16384, 1024, 128, fake, 128, 128,
-                                 fake, fake, 2048, 128, None, 0, 32, 16, 8, 128, 16, 4096, 0,
-                                 1.0, 2, None)
+                                 fake, fake, 2048, 128, None, 0, None, 32, 16, 8, 128, 16, 4096,
+                                 0, 1.0, 2, None)
     assert status == 3 and "workspace" in _lib.last_error()
+    status = lib.mi_paged_decode(fake, 2048, 128, fake, fake, 16384, 1024, 128, fake, 128, 128,
+                                 fake, fake, 2048, 128, fake, need, None, 32, 16, 8, 128, 16,
+                                 4096, 0, 1.0, 2, None)
+    assert status == 3 and "counters" in _lib.last_error()
 
 
 @pytest.mark.parametrize("split_k,expect_zero", [(1, True), (0, False), (4, False)])

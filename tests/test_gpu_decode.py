@@ -225,6 +225,26 @@ def test_poison_is_never_read_and_bad_table_entries_are_masked():
     assert torch.isfinite(out).all()
 
 
+def test_split_counters_are_left_zeroed():
+    from microinfer_amd.layer import hip_paged_attention as ops
+
+    torch.manual_seed(6)
+    kc = torch.randn(300, 16, 8, 128, device=DEV).to(torch.bfloat16)
+    vc = torch.randn_like(kc)
+    q = torch.randn(3, 32, 128, device=DEV).to(torch.bfloat16)
+    tables = torch.randperm(300, device=DEV)[:300].reshape(3, 100).to(torch.int32)
+    lens = torch.tensor([1600, 7, 900], dtype=torch.int32, device=DEV)
+    first = hip_paged_decode(q, kc, vc, tables, lens, split_k=16)
+    second = hip_paged_decode(q, kc, vc, tables, lens, split_k=16)
+    third = hip_paged_decode(q, kc, vc, tables, lens)
+    torch.cuda.synchronize()
+    assert torch.equal(first, second)
+    for counters in ops._counters.values():
+        assert int(counters.abs().sum()) == 0
+    expected = oracle_decode(q, kc, vc, tables, lens, 1 / math.sqrt(128))
+    assert max_abs(first, expected) <= 2e-2 and max_abs(third, expected) <= 2e-2
+
+
 def test_hipgraph_replay_tracks_new_contexts():
     torch.manual_seed(5)
     kc = torch.randn(512, 16, 8, 128, device=DEV).to(torch.bfloat16)
