@@ -157,7 +157,7 @@ def main() -> int:
     import torch
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from microinfer_amd.layer.hip_paged_attention import hip_paged_decode
+    from microinfer_amd.layer.hip_paged_attention import decode_plan, hip_paged_decode
     from microinfer_amd.workloads import decode_bytes
 
     log("allocating 28-layer caches")
@@ -168,11 +168,15 @@ def main() -> int:
     outputs = []
 
     def step():
+        # One partition plan per step, shared by the 28 layers (as the
+        # engine's AttentionMetadata does).
+        plan = decode_plan(lens, num_kv_heads=8, block_size=16,
+                           block_table_width=tables.shape[1])
         outputs.clear()
         for layer, view in enumerate(views):
             view.write_slots(slots, new_k[layer], new_v[layer])
             outputs.append(hip_paged_decode(query[layer], view.keys, view.values, tables, lens,
-                                            scale=scale))
+                                            scale=scale, plan=plan))
 
     step()
     torch.cuda.synchronize()

@@ -94,19 +94,39 @@ int32_t mi_kv_append(const void* keys, int64_t key_token_stride, int64_t key_hea
  * publishes its online-softmax state to `workspace` and bumps an arrival
  * counter; the last arrival merges all of them and writes the output.
  *
- * workspace: float32 device buffer of at least
- * mi_paged_decode_workspace_bytes(...) bytes, 256-byte aligned (may be NULL
- * when that is 0); no initialisation needed.
+ * workspace: device buffer of at least mi_paged_decode_workspace_bytes(...)
+ * bytes, 256-byte aligned; no initialisation needed. It holds the split
+ * partials and, when `plan` is NULL, the plan this call computes first.
  * counters: int32 device array of at least num_seqs * num_kv_heads entries
  * that must be ZERO on entry; every call leaves it zero again, so one array
  * can serve all later calls on the same stream. Calls that run concurrently
- * (different streams) need separate counters and workspaces. May be NULL
- * when the workspace size is 0.
+ * (different streams) need separate counters and workspaces.
+ * plan: NULL, or a plan from mi_decode_plan for this step (see there) in a
+ * buffer of plan_bytes >= mi_decode_plan_bytes(...) under the current tuning.
  * Sequences with context_len 0 produce zeros.
  */
 int64_t mi_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
                                         int32_t num_kv_heads, int32_t head_dim,
                                         int32_t split_k);
+
+/*
+ * Decode partition plan: the list of (sequence, block range) work items that
+ * mi_paged_decode runs, derived on the device from context_lens. All layers
+ * of a step share one plan, so an engine computes it once per step and
+ * passes it to every layer's mi_paged_decode (which otherwise computes it
+ * into its workspace on every call). Sequences are ordered longest first, so
+ * split sequences finish (and merge) while shorter items still stream.
+ * plan: device buffer of at least mi_decode_plan_bytes(...) bytes; the
+ * result is valid for calls with the same context_lens contents, num_seqs,
+ * num_kv_heads, block_size, block_table_width and split_k. A plan that does
+ * not match produces wrong attention but never reads out of bounds.
+ * At most 4096 sequences.
+ */
+int64_t mi_decode_plan_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t split_k);
+
+int32_t mi_decode_plan(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
+                       int32_t block_size, int32_t block_table_width, int32_t split_k,
+                       void* plan, int64_t plan_bytes, void* stream);
 
 /*
  * Tuning of the adaptive partition plan (split_k = 0): aim for about
@@ -124,10 +144,11 @@ int32_t mi_paged_decode(const void* query, int64_t q_token_stride, int64_t q_hea
                         int64_t block_table_stride, int32_t block_table_width,
                         const int32_t* context_lens, void* out, int64_t out_token_stride,
                         int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
-                        int32_t* counters, int32_t num_seqs, int32_t num_q_heads,
-                        int32_t num_kv_heads,
-                        int32_t head_dim, int32_t block_size, int32_t num_blocks,
-                        int32_t split_k, float scale, int32_t dtype, void* stream);
+                        int32_t* counters, const void* plan, int64_t plan_bytes,
+                        int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                        int32_t head_dim,
+                        int32_t block_size, int32_t num_blocks, int32_t split_k,
+                        float scale, int32_t dtype, void* stream);
 
 /*
  * Paged varlen (prefill / mixed) attention with a bottom-right causal mask:

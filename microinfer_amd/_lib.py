@@ -39,8 +39,10 @@ SIGNATURES = {
     "mi_paged_decode": (
         _I32,
         [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P, _P, _I64, _I64,
-         _P, _I64, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P],
+         _P, _I64, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P],
     ),
+    "mi_decode_plan_bytes": (_I64, [_I32, _I32, _I32]),
+    "mi_decode_plan": (_I32, [_P, _I32, _I32, _I32, _I32, _I32, _P, _I64, _P]),
     "mi_paged_prefill": (
         _I32,
         [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _I32, _P, _I64,

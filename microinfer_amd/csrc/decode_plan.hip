@@ -1,0 +1,194 @@
+// Decode partition plan: which (sequence, block range) work items a paged
+// decode launch runs. Computed on the device from context_lens, so a
+// hipGraph replays it with whatever lengths the step has.
+//
+// The reference fixes split_k per launch on the host from R * Hq
+// (microinfer/layer/triton_paged_attention.py:342-349) and stripes tiles over
+// the splits (:76-79). Here partitions are contiguous block ranges sized from
+// the step's total context: about target_items (item, KV head) workgroups of
+// at least min_part_blocks blocks each. Sequences are ordered longest first,
+// so the partitions of split sequences run (and merge) early while shorter
+// single-partition items keep the memory system busy at the end.
+#include "paged_attention.h"
+
+namespace mi {
+namespace {
+
+int32_t g_target_items = 512;
+int32_t g_min_part_blocks = 4;
+
+constexpr int kPlanThreads = 1024;
+constexpr int kSortLimit = 1024;  // larger batches keep submission order
+
+__device__ __forceinline__ int blocks_of(int ctx, int block_size, int lb) {
+  return (ctx + block_size - 1) >> lb;
+}
+
+__device__ __forceinline__ int part_blocks(int nb, int split_k, int pb_global) {
+  if (split_k == 0) return pb_global;
+  const int k = min(split_k, max(nb, 1));
+  return max(1, (nb + k - 1) / k);
+}
+
+__global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
+    const int32_t* __restrict__ context_lens, int num_seqs, int num_kv_heads, int block_size,
+    int lb, int width, int split_k, int target, int min_pb, int max_items,
+    PlanItem* __restrict__ plan) {
+  __shared__ int s_ctx[kMaxPlanSeqs];
+  __shared__ int s_order[kMaxPlanSeqs];  // rank -> sequence
+  __shared__ int s_first[kMaxPlanSeqs];  // rank -> first item index
+  __shared__ int s_scan[kPlanThreads];
+  __shared__ int s_total_blocks;
+  __shared__ int s_total_items;
+  const int tid = threadIdx.x;
+  const int max_ctx = width * block_size;
+
+  if (tid == 0) {
+    s_total_blocks = 0;
+    s_total_items = 0;
+  }
+  __syncthreads();
+  int local = 0;
+  for (int r = tid; r < num_seqs; r += kPlanThreads) {
+    const int c = min(max(context_lens[r], 0), max_ctx);
+    s_ctx[r] = c;
+    local += blocks_of(c, block_size, lb);
+  }
+  atomicAdd(&s_total_blocks, local);
+  __syncthreads();
+  int pb_global = 1;
+  if (split_k == 0) {
+    const int64_t want = static_cast<int64_t>(s_total_blocks) * num_kv_heads;
+    pb_global = max(min_pb, max(1, static_cast<int>((want + target - 1) / target)));
+  }
+
+  // Rank sequences by block count, longest first (ties keep batch order).
+  const bool sort = num_seqs <= kSortLimit;
+  for (int r = tid; r < num_seqs; r += kPlanThreads) {
+    int rank = r;
+    if (sort) {
+      const int nb = blocks_of(s_ctx[r], block_size, lb);
+      rank = 0;
+      for (int s = 0; s < num_seqs; ++s) {
+        const int ns = blocks_of(s_ctx[s], block_size, lb);
+        rank += (ns > nb) || (ns == nb && s < r);
+      }
+    }
+    s_order[rank] = r;
+  }
+  __syncthreads();
+
+  // Exclusive scan of partition counts in rank order: each thread owns a run
+  // of consecutive ranks, then the per-thread sums are scanned in LDS.
+  const int per = (num_seqs + kPlanThreads - 1) / kPlanThreads;
+  const int k0 = tid * per;
+  const int k1 = min(num_seqs, k0 + per);
+  int run = 0;
+  for (int k = k0; k < k1; ++k) {
+    const int nb = blocks_of(s_ctx[s_order[k]], block_size, lb);
+    run += max(1, (nb + part_blocks(nb, split_k, pb_global) - 1) /
+                      part_blocks(nb, split_k, pb_global));
+  }
+  s_scan[tid] = run;
+  __syncthreads();
+  for (int off = 1; off < kPlanThreads; off <<= 1) {
+    const int v = tid >= off ? s_scan[tid - off] : 0;
+    __syncthreads();
+    s_scan[tid] += v;
+    __syncthreads();
+  }
+  int first = s_scan[tid] - run;
+  for (int k = k0; k < k1; ++k) {
+    s_first[k] = first;
+    const int nb = blocks_of(s_ctx[s_order[k]], block_size, lb);
+    const int pb = part_blocks(nb, split_k, pb_global);
+    first += max(1, (nb + pb - 1) / pb);
+  }
+  if (tid == kPlanThreads - 1) s_total_items = s_scan[tid];
+  __syncthreads();
+
+  // Emit the items, then mark the rest of the launch's slots unused.
+  for (int k = tid; k < num_seqs; k += kPlanThreads) {
+    const int r = s_order[k];
+    const int c = s_ctx[r];
+    const int nb = blocks_of(c, block_size, lb);
+    const int pb = part_blocks(nb, split_k, pb_global);
+    const int np = max(1, (nb + pb - 1) / pb);
+    const int f = s_first[k];
+    for (int p = 0; p < np && f + p < max_items; ++p) {
+      PlanItem it;
+      it.seq = r;
+      it.blk_begin = p * pb;
+      it.blk_end = min(nb, (p + 1) * pb);
+      it.nparts = np;
+      it.first_item = f;
+      it.ctx = c;
+      it.part = p;
+      it.unused = 0;
+      plan[f + p] = it;
+    }
+  }
+  for (int i = s_total_items + tid; i < max_items; i += kPlanThreads) {
+    PlanItem it{};
+    it.seq = -1;
+    plan[i] = it;
+  }
+}
+
+}  // namespace
+
+int32_t decode_max_items(int32_t num_seqs, int32_t num_kv_heads, int32_t split_k) {
+  if (split_k > 0) return num_seqs * split_k;
+  return (g_target_items + num_kv_heads - 1) / num_kv_heads + num_seqs;
+}
+
+int64_t decode_plan_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t split_k) {
+  return static_cast<int64_t>(decode_max_items(num_seqs, num_kv_heads, split_k)) *
+         static_cast<int64_t>(sizeof(PlanItem));
+}
+
+int32_t launch_decode_plan(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
+                           int32_t block_size, int32_t block_table_width, int32_t split_k,
+                           PlanItem* plan, hipStream_t stream) {
+  decode_plan_kernel<<<1, kPlanThreads, 0, stream>>>(
+      context_lens, num_seqs, num_kv_heads, block_size, ilog2(block_size), block_table_width,
+      split_k, g_target_items, g_min_part_blocks,
+      decode_max_items(num_seqs, num_kv_heads, split_k), plan);
+  return check_launch("decode plan");
+}
+
+}  // namespace mi
+
+extern "C" void mi_tune_decode(int32_t target_items, int32_t min_part_blocks) {
+  if (target_items > 0) mi::g_target_items = target_items;
+  if (min_part_blocks > 0) mi::g_min_part_blocks = min_part_blocks;
+}
+
+extern "C" int64_t mi_decode_plan_bytes(int32_t num_seqs, int32_t num_kv_heads,
+                                        int32_t split_k) {
+  if (num_seqs <= 0 || num_kv_heads <= 0 || split_k < 0) return 0;
+  return mi::decode_plan_bytes(num_seqs, num_kv_heads, split_k);
+}
+
+extern "C" int32_t mi_decode_plan(const int32_t* context_lens, int32_t num_seqs,
+                                  int32_t num_kv_heads, int32_t block_size,
+                                  int32_t block_table_width, int32_t split_k, void* plan,
+                                  int64_t plan_bytes, void* stream) {
+  using namespace mi;
+  clear_error();
+  if (num_seqs < 0 || num_kv_heads <= 0 || split_k < 0 || block_table_width < 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_decode_plan: invalid sizes");
+  if (!is_pow2(block_size))
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_decode_plan: block_size must be a power of two");
+  if (num_seqs > kMaxPlanSeqs)
+    return fail(MI_ERR_UNSUPPORTED, "mi_decode_plan: more than 4096 sequences");
+  if (num_seqs == 0) return MI_OK;
+  if (!context_lens || !plan)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_decode_plan: null pointer");
+  if (plan_bytes < decode_plan_bytes(num_seqs, num_kv_heads, split_k) ||
+      reinterpret_cast<uintptr_t>(plan) % 32 != 0)
+    return fail(MI_ERR_WORKSPACE, "mi_decode_plan: plan buffer too small or misaligned");
+  return launch_decode_plan(context_lens, num_seqs, num_kv_heads, block_size,
+                            block_table_width, split_k, static_cast<PlanItem*>(plan),
+                            static_cast<hipStream_t>(stream));
+}

@@ -61,6 +61,10 @@ struct F16 {
   }
 };
 
+// 2^x with the hardware v_exp_f32 (about 1 ulp; results below the normal
+// range flush to zero, which only affects weights already < 2^-126).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // N consecutive raw elements moved with one load/store instruction.
 template <typename R, int N>
 struct alignas(sizeof(R) * N) Pack {
@@ -75,6 +79,21 @@ __device__ __forceinline__ Pack<R, N> load_pack(const R* p) {
 template <typename R, int N>
 __device__ __forceinline__ void store_pack(R* p, const Pack<R, N>& v) {
   *reinterpret_cast<Pack<R, N>*>(p) = v;
+}
+
+// Scheduling fence for loaded registers: an empty asm that "rewrites" every
+// dword of the pack, so no instruction that uses the pack can be moved above
+// this point. Double-buffered loops call it where a buffer starts being
+// consumed, which keeps the compiler from waiting on the buffer that is
+// still in flight.
+template <typename R, int N>
+__device__ __forceinline__ void pin(Pack<R, N>& p) {
+  constexpr int W = sizeof(Pack<R, N>) / 4;
+  static_assert(sizeof(Pack<R, N>) % 4 == 0, "pack must be whole dwords");
+  Pack<uint32_t, W> w = __builtin_bit_cast(Pack<uint32_t, W>, p);
+#pragma unroll
+  for (int i = 0; i < W; ++i) asm volatile("" : "+v"(w.v[i]));
+  p = __builtin_bit_cast(Pack<R, N>, w);
 }
 
 template <typename R, int N>

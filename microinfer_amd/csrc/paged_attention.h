@@ -5,6 +5,13 @@
 
 namespace mi {
 
+// One decode work item: blocks [blk_begin, blk_end) of sequence `seq`, which
+// is split into `nparts` partitions numbered first_item .. first_item+nparts-1
+// (this one is partition `part`). seq < 0 marks an unused slot.
+struct alignas(32) PlanItem {
+  int32_t seq, blk_begin, blk_end, nparts, first_item, ctx, part, unused;
+};
+
 // Arguments of the vector (non-MFMA) paged attention kernels. Strides are in
 // elements; head_dim is contiguous everywhere.
 struct AttnArgs {
@@ -24,6 +31,12 @@ struct AttnArgs {
   float* ws_acc;  // split partials: [items, Hkv, G, D] unnormalised sums
   float* ws_ml;   // split partials: [items, Hkv, G, 2] (log2-domain max, sum)
   int32_t* counters;  // [num_seqs * Hkv] arrival counts; zero on entry and exit
+  const PlanItem* plan;  // decode: [max_items] work items
+  // Decode with fused append (optional): row s of new_k/new_v is written to
+  // position ctx_s - 1 of sequence s and attended to from registers.
+  const void* new_k;
+  const void* new_v;
+  int64_t nk_ts, nk_hs, nv_ts, nv_hs;
   int32_t num_seqs;  // decode: sequences; varlen: requests
   int32_t num_rows;  // varlen: query rows
   int32_t num_kv_heads, group, head_dim, block_size, log2_block, num_blocks;
@@ -40,7 +53,16 @@ struct AttnArgs {
 int32_t launch_paged_attention_vector(const AttnArgs& args, int32_t dtype,
                                       hipStream_t stream);
 
-// Upper bound on decode work items for a launch (grid.x).
+// Upper bound on decode work items for a launch (grid.x / Hkv).
 int32_t decode_max_items(int32_t num_seqs, int32_t num_kv_heads, int32_t split_k);
+
+// Plan size and launch (decode_plan.hip). The plan has decode_max_items()
+// entries; unused ones carry seq = -1.
+int64_t decode_plan_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t split_k);
+int32_t launch_decode_plan(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
+                           int32_t block_size, int32_t block_table_width, int32_t split_k,
+                           PlanItem* plan, hipStream_t stream);
+
+constexpr int32_t kMaxPlanSeqs = 4096;
 
 }  // namespace mi

@@ -11,12 +11,6 @@ int32_t launch_vector_bf16(const AttnArgs& a, hipStream_t stream);
 
 namespace {
 
-// Adaptive split-K tuning: the decode launch aims for about g_target_items
-// (work item, KV head) workgroups, each covering at least g_min_part_blocks
-// blocks.
-int32_t g_target_items = 512;
-int32_t g_min_part_blocks = 4;
-
 constexpr float kLog2e = 1.4426950408889634f;
 
 int32_t dispatch_vector(const AttnArgs& a, int32_t dtype, hipStream_t stream) {
@@ -51,29 +45,29 @@ bool aligned(const void* p, int64_t bytes) {
   return (reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(bytes)) == 0;
 }
 
+// Workspace layout: [plan (256-byte aligned)][acc partials][(m, l) partials].
+int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+int64_t partial_floats(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                       int32_t head_dim, int32_t split_k) {
+  if (split_k == 1) return 0;  // one partition per sequence: no partials
+  const int64_t items = decode_max_items(num_seqs, num_kv_heads, split_k);
+  const int64_t group = num_q_heads / num_kv_heads;
+  return items * num_kv_heads * group * (head_dim + 2);
+}
+
 }  // namespace
-
-int32_t decode_max_items(int32_t num_seqs, int32_t num_kv_heads, int32_t split_k) {
-  if (split_k > 0) return num_seqs * split_k;
-  return (g_target_items + num_kv_heads - 1) / num_kv_heads + num_seqs;
-}
-
 }  // namespace mi
-
-extern "C" void mi_tune_decode(int32_t target_items, int32_t min_part_blocks) {
-  if (target_items > 0) mi::g_target_items = target_items;
-  if (min_part_blocks > 0) mi::g_min_part_blocks = min_part_blocks;
-}
 
 extern "C" int64_t mi_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
                                                    int32_t num_kv_heads, int32_t head_dim,
                                                    int32_t split_k) {
+  using namespace mi;
   if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || head_dim <= 0 || split_k < 0)
     return 0;
-  if (split_k == 1) return 0;  // one partition per sequence: no partials
-  const int64_t items = mi::decode_max_items(num_seqs, num_kv_heads, split_k);
-  const int64_t group = num_q_heads / num_kv_heads;
-  return items * num_kv_heads * group * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
+  return round_up(decode_plan_bytes(num_seqs, num_kv_heads, split_k), 256) +
+         partial_floats(num_seqs, num_q_heads, num_kv_heads, head_dim, split_k) *
+             static_cast<int64_t>(sizeof(float));
 }
 
 extern "C" int32_t mi_paged_decode(
@@ -82,10 +76,10 @@ extern "C" int32_t mi_paged_decode(
     int64_t cache_head_stride, const int32_t* block_tables, int64_t block_table_stride,
     int32_t block_table_width, const int32_t* context_lens, void* out,
     int64_t out_token_stride, int64_t out_head_stride, void* workspace,
-    int64_t workspace_bytes, int32_t* counters, int32_t num_seqs, int32_t num_q_heads,
-    int32_t num_kv_heads,
-    int32_t head_dim, int32_t block_size, int32_t num_blocks, int32_t split_k, float scale,
-    int32_t dtype, void* stream) {
+    int64_t workspace_bytes, int32_t* counters, const void* plan, int64_t plan_bytes,
+    int32_t num_seqs,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+    int32_t num_blocks, int32_t split_k, float scale, int32_t dtype, void* stream) {
   using namespace mi;
   clear_error();
   int32_t st = check_common("mi_paged_decode", dtype, num_q_heads, num_kv_heads, head_dim,
@@ -94,6 +88,8 @@ extern "C" int32_t mi_paged_decode(
   if (num_seqs < 0 || split_k < 0)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode: negative num_seqs or split_k");
   if (num_seqs == 0) return MI_OK;
+  if (num_seqs > kMaxPlanSeqs)
+    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode: more than 4096 sequences");
   if (!query || !key_cache || !value_cache || !block_tables || !context_lens || !out)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode: null pointer");
   const int64_t es = static_cast<int64_t>(dtype_size(dtype));
@@ -106,11 +102,18 @@ extern "C" int32_t mi_paged_decode(
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode: misaligned pointers or strides");
   const int64_t need = mi_paged_decode_workspace_bytes(num_seqs, num_q_heads, num_kv_heads,
                                                        head_dim, split_k);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 256)))
+  if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 256))
     return fail(MI_ERR_WORKSPACE, "mi_paged_decode: workspace needs " +
                                       std::to_string(need) + " bytes (256-byte aligned)");
-  if (need > 0 && counters == nullptr)
+  const int64_t partials =
+      partial_floats(num_seqs, num_q_heads, num_kv_heads, head_dim, split_k);
+  if (partials > 0 && counters == nullptr)
     return fail(MI_ERR_WORKSPACE, "mi_paged_decode: split partitions need zeroed counters");
+  if (plan != nullptr &&
+      (!aligned(plan, 32) || plan_bytes < decode_plan_bytes(num_seqs, num_kv_heads, split_k)))
+    return fail(MI_ERR_INVALID_ARGUMENT,
+                "mi_paged_decode: plan must be 32-byte aligned and sized by "
+                "mi_decode_plan_bytes for this call");
 
   AttnArgs a{};
   a.q = query;
@@ -136,19 +139,29 @@ extern "C" int32_t mi_paged_decode(
   a.log2_block = ilog2(block_size);
   a.num_blocks = num_blocks;
   a.split_k = split_k;
-  a.target_items = g_target_items;
-  a.min_part_blocks = g_min_part_blocks;
-  a.max_items = decode_max_items(num_seqs, num_kv_heads, split_k == 1 ? 1 : split_k);
+  a.max_items = decode_max_items(num_seqs, num_kv_heads, split_k);
   a.scale_log2 = scale * kLog2e;
   a.varlen = 0;
-  if (need > 0) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const int64_t plan_region = round_up(decode_plan_bytes(num_seqs, num_kv_heads, split_k), 256);
+  if (plan == nullptr) {
+    PlanItem* own = reinterpret_cast<PlanItem*>(ws);
+    st = launch_decode_plan(context_lens, num_seqs, num_kv_heads, block_size,
+                            block_table_width, split_k, own, s);
+    if (st != MI_OK) return st;
+    a.plan = own;
+  } else {
+    a.plan = static_cast<const PlanItem*>(plan);
+  }
+  if (partials > 0) {
     const int64_t acc_floats =
         static_cast<int64_t>(a.max_items) * num_kv_heads * a.group * head_dim;
-    a.ws_acc = static_cast<float*>(workspace);
+    a.ws_acc = reinterpret_cast<float*>(ws + plan_region);
     a.ws_ml = a.ws_acc + acc_floats;
     a.counters = counters;
   }
-  return dispatch_vector(a, dtype, static_cast<hipStream_t>(stream));
+  return dispatch_vector(a, dtype, s);
 }
 
 extern "C" int32_t mi_paged_prefill(

@@ -15,11 +15,11 @@
 //    in registers: tile i+1 is in flight while tile i is computed.
 //  * Scores: per-lane partial dot products summed over the LPR lanes of a row
 //    with DPP. Each lane group (PPW of them per wave) keeps its own
-//    online-softmax state in the log2 domain (q is pre-scaled by scale*log2 e);
-//    the groups are merged once at the end.
-//  * Partitions are planned on the device from context_lens: every wave
-//    recomputes the same prefix sum over sequences, so the launch shape
-//    depends only on the batch size and stays valid under hipGraph replay.
+//    online-softmax state in the log2 domain; the groups, then the waves of
+//    a workgroup (through LDS), are merged once at the end.
+//  * Decode work items come from a plan computed on the device from
+//    context_lens (decode_plan.hip), so the launch shape depends only on the
+//    batch size and stays valid under hipGraph replay.
 //  * Partitions of one (sequence, KV head) are merged in the same launch: each
 //    publishes (acc, m, l) with L2-coherent stores and bumps an arrival
 //    counter; the last arrival merges and writes the output, then re-zeroes
@@ -29,72 +29,6 @@
 #include "paged_attention.h"
 
 namespace mi {
-
-struct WorkItem {
-  int seq, part, nparts, blk_begin, blk_end, ctx;
-};
-
-// Decode plan, computed identically by every wave of a launch.
-//  nb_r  = ceil(min(ctx_r, width * B) / B) blocks of sequence r
-//  PB    = adaptive: max(min_part_blocks, ceil(sum nb * Hkv / target_items))
-//          forced:   ceil(nb_r / min(split_k, nb_r)) per sequence
-//  parts_r = max(1, ceil(nb_r / PB)); items are numbered sequence-major.
-// Finds work item `key`; returns false when the launch has fewer items.
-__device__ __forceinline__ bool decode_plan(const AttnArgs& a, int key, int lane, WorkItem& it) {
-  const int B = a.block_size;
-  const int lb = a.log2_block;
-  const int max_ctx = a.t_width * B;
-  int pb_global = 1;
-  if (a.split_k == 0) {
-    int total = 0;
-    for (int base = 0; base < a.num_seqs; base += kWave) {
-      const int r = base + lane;
-      if (r < a.num_seqs) {
-        const int c = min(max(a.ctx[r], 0), max_ctx);
-        total += (c + B - 1) >> lb;
-      }
-    }
-    total = wave_sum_int(total);
-    const int64_t want = static_cast<int64_t>(total) * a.num_kv_heads;
-    const int pb = static_cast<int>((want + a.target_items - 1) / a.target_items);
-    pb_global = max(a.min_part_blocks, max(pb, 1));
-  }
-  int running = 0;
-  for (int base = 0; base < a.num_seqs; base += kWave) {
-    const int r = base + lane;
-    int c = 0, nb = 0, pb = 1, np = 0;
-    if (r < a.num_seqs) {
-      c = min(max(a.ctx[r], 0), max_ctx);
-      nb = (c + B - 1) >> lb;
-      if (a.split_k == 0) {
-        pb = pb_global;
-      } else {
-        const int k = min(a.split_k, max(nb, 1));
-        pb = max(1, (nb + k - 1) / k);
-      }
-      np = max(1, (nb + pb - 1) / pb);
-    }
-    const int incl = wave_inclusive_scan(np, lane);
-    const int start = running + incl - np;
-    const bool mine = (r < a.num_seqs) && key >= start && key < start + np;
-    const uint64_t hit = __ballot(mine);
-    if (hit) {
-      const int src = __ffsll(static_cast<unsigned long long>(hit)) - 1;
-      const int first = __shfl(start, src, kWave);
-      const int pbs = __shfl(pb, src, kWave);
-      const int nbs = __shfl(nb, src, kWave);
-      it.seq = __shfl(r, src, kWave);
-      it.nparts = __shfl(np, src, kWave);
-      it.ctx = __shfl(c, src, kWave);
-      it.part = key - first;
-      it.blk_begin = it.part * pbs;
-      it.blk_end = min(nbs, it.blk_begin + pbs);
-      return true;
-    }
-    running += __shfl(incl, kWave - 1, kWave);
-  }
-  return false;
-}
 
 // One double-buffer slot: UNROLL K and V packs plus a validity bit per load.
 template <typename R, int VEC, int UNROLL>
@@ -111,16 +45,18 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
   constexpr int D = VEC * LPR;
   constexpr int PPW = kWave / LPR;  // rows per load instruction
   constexpr int TILE = PPW * UNROLL;
-  const int wave = threadIdx.x / kWave;
+  // readfirstlane tells the compiler the wave index is uniform, which keeps
+  // tile positions and block-id lookups scalar.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
   const int grp = lane / LPR;
   const int sub = lane % LPR;
   const int d0 = sub * VEC;
-  const int head = blockIdx.y;
-  const int w = blockIdx.x;
+  // Flattened grid: consecutive workgroups are the KV heads of one item.
+  const int head = blockIdx.x % a.num_kv_heads;
+  const int w = blockIdx.x / a.num_kv_heads;
   const int G = EXACT ? GMAX : a.group;
 
-  // Every wave derives the same work item, so no barrier is needed here.
   int seq, q_row, ctx, blk_begin, blk_end, nparts, first_item = 0;
   if (a.varlen) {
     q_row = w;
@@ -139,16 +75,23 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
     blk_end = (ctx + a.block_size - 1) >> a.log2_block;
     nparts = 1;
   } else {
-    WorkItem it;
-    if (!decode_plan(a, w, lane, it)) return;  // uniform across the workgroup
-    // The plan is identical on every lane; keep it in scalar registers.
-    seq = __builtin_amdgcn_readfirstlane(it.seq);
+    // Work item from the step's plan (one scalar load). Items are validated so
+    // that a stale or foreign plan can give wrong attention but never an
+    // out-of-bounds access.
+    typedef int32_t int8v __attribute__((ext_vector_type(8)));
+    using ConstItem = __attribute__((address_space(4))) const int8v;
+    static_assert(sizeof(PlanItem) == sizeof(int8v), "plan item is eight int32");
+    const PlanItem it = __builtin_bit_cast(PlanItem, ((ConstItem*)(a.plan))[w]);  // C cast: address space
+    if (it.seq < 0 || it.seq >= a.num_seqs || it.nparts < 1 || it.part < 0 ||
+        it.part >= it.nparts || it.first_item < 0 || it.first_item + it.nparts > a.max_items)
+      return;  // unused slot (uniform across the workgroup)
+    seq = it.seq;
     q_row = seq;
-    ctx = __builtin_amdgcn_readfirstlane(it.ctx);
-    blk_begin = __builtin_amdgcn_readfirstlane(it.blk_begin);
-    blk_end = __builtin_amdgcn_readfirstlane(it.blk_end);
-    nparts = __builtin_amdgcn_readfirstlane(it.nparts);
-    first_item = w - __builtin_amdgcn_readfirstlane(it.part);
+    ctx = min(max(it.ctx, 0), a.t_width * a.block_size);
+    blk_begin = max(it.blk_begin, 0);
+    blk_end = min(it.blk_end, a.t_width);
+    nparts = it.nparts;
+    first_item = it.first_item;
   }
 
   // Query rows of the G heads. 16-bit types keep raw element pairs for the
@@ -246,7 +189,14 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
   };
 
   // Online softmax + P.V over one loaded tile (this lane group's positions).
-  auto consume = [&](const Tile& T) {
+  auto consume = [&](Tile& T) {
+    // Nothing that reads this tile may be scheduled before this point (in
+    // particular not next to the loads of the other, still in-flight tile).
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      pin(T.k[u]);
+      pin(T.v[u]);
+    }
     float s[UNROLL][GMAX];
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
@@ -274,14 +224,14 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
 #pragma unroll
       for (int u = 1; u < UNROLL; ++u) tmax = fmaxf(tmax, s[u][g]);
       const float mnew = fmaxf(m[g], tmax);
-      const float alpha = (mnew == -INFINITY) ? 1.f : exp2f(m[g] - mnew);
+      const float alpha = (mnew == -INFINITY) ? 1.f : fast_exp2(m[g] - mnew);
       m[g] = mnew;
       lsum[g] *= alpha;
 #pragma unroll
       for (int j = 0; j < VEC; ++j) acc[g][j] *= alpha;
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) {
-        const float p = ((T.ok >> u) & 1u) ? exp2f(s[u][g] - mnew) : 0.f;
+        const float p = ((T.ok >> u) & 1u) ? fast_exp2(s[u][g] - mnew) : 0.f;
         lsum[g] += p;
 #pragma unroll
         for (int j = 0; j < VEC; ++j) acc[g][j] = fmaf(p, E::load(T.v[u].v[j]), acc[g][j]);
@@ -292,6 +242,9 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
   // Double-buffered tile loop. The NW waves interleave the partition's tiles
   // (wave k takes tiles k, k + NW, ...); tile i+1 is in flight while tile i is
   // used.
+  // The next tile is issued unconditionally (past the end its loads hit the
+  // safe row and are masked), so every path through the loop has the same
+  // loads in flight and the wait counts stay exact.
   constexpr int STRIDE = TILE * NW;
   if (pos_begin + wave * TILE < pos_end) {
     Tile A, B;
@@ -299,15 +252,13 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
     issue(A, t0);
     while (true) {
       const int t1 = t0 + STRIDE;
-      const bool more = t1 < pos_end;
-      if (more) issue(B, t1);
+      issue(B, t1);
       consume(A);
-      if (!more) break;
+      if (t1 >= pos_end) break;
       const int t2 = t1 + STRIDE;
-      const bool more2 = t2 < pos_end;
-      if (more2) issue(A, t2);
+      issue(A, t2);
       consume(B);
-      if (!more2) break;
+      if (t2 >= pos_end) break;
       t0 = t2;
     }
   }
@@ -317,7 +268,7 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
 #pragma unroll
   for (int g = 0; g < GMAX; ++g) {
     const float mw = xor_max<LPR, kWave>(m[g]);
-    const float f = (m[g] == -INFINITY) ? 0.f : exp2f(m[g] - mw);
+    const float f = (m[g] == -INFINITY) ? 0.f : fast_exp2(m[g] - mw);
     m[g] = mw;
     lsum[g] = xor_sum<LPR, kWave>(lsum[g] * f);
 #pragma unroll
@@ -354,7 +305,7 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
 #pragma unroll
       for (int k = 0; k < NW; ++k) {
         const float mk = s_ml[k][g][0];
-        const float f = (mk == -INFINITY) ? 0.f : exp2f(mk - mx);
+        const float f = (mk == -INFINITY) ? 0.f : fast_exp2(mk - mx);
         l = fmaf(f, s_ml[k][g][1], l);
 #pragma unroll
         for (int j = 0; j < VEC; ++j) o[j] = fmaf(f, s_acc[k][g][d0 + j], o[j]);
@@ -447,7 +398,7 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
       if ((EXACT || g < G) && i < nparts) {
         const float mi = load_coherent(a.ws_ml + item_row(i, g) * 2);
         const float li = load_coherent(a.ws_ml + item_row(i, g) * 2 + 1);
-        wgt[g] = (mi == -INFINITY) ? 0.f : exp2f(mi - mx[g]);
+        wgt[g] = (mi == -INFINITY) ? 0.f : fast_exp2(mi - mx[g]);
         total[g] = fmaf(wgt[g], li, total[g]);
       }
     }
@@ -521,7 +472,7 @@ int32_t launch_vector_typed(const AttnArgs& a, hipStream_t stream) {
   constexpr int kPackElems = 16 / sizeof(R);
   const int D = a.head_dim;
   const int G = a.group;
-  const dim3 grid(a.varlen ? a.num_rows : a.max_items, a.num_kv_heads);
+  const dim3 grid((a.varlen ? a.num_rows : a.max_items) * a.num_kv_heads);
   bool launched = false;
 
 #define MI_VEC_LAUNCH(DIM, GM, EX)                                                     \

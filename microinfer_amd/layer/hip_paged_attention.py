@@ -90,6 +90,28 @@ def decode_workspace_bytes(num_seqs: int, num_q_heads: int, num_kv_heads: int,
     )
 
 
+def decode_plan(context_lens: torch.Tensor, *, num_kv_heads: int, block_size: int,
+                block_table_width: int, split_k: int | None = None) -> torch.Tensor:
+    """Partition plan for one decode step (shared by every layer of the step).
+
+    Computed on the device from ``context_lens`` (int32 ``[R]``), so it can be
+    captured in a hipGraph; pass it to ``hip_paged_decode(..., plan=...)``.
+    """
+    _lib.require_device(context_lens, what="decode_plan")
+    context_lens = _index32(context_lens)
+    num_seqs = context_lens.numel()
+    split = 0 if split_k is None else split_k
+    lib = _lib.load()
+    nbytes = int(lib.mi_decode_plan_bytes(num_seqs, num_kv_heads, split))
+    plan = torch.empty(max(nbytes, 32), dtype=torch.uint8, device=context_lens.device)
+    status = lib.mi_decode_plan(
+        context_lens.data_ptr(), num_seqs, num_kv_heads, block_size, block_table_width, split,
+        plan.data_ptr(), plan.numel(), _lib.stream_handle(context_lens.device),
+    )
+    _lib.check(status, "mi_decode_plan")
+    return plan
+
+
 def hip_paged_decode(
     query: torch.Tensor,
     key_cache: torch.Tensor,
@@ -99,12 +121,15 @@ def hip_paged_decode(
     *,
     scale: float | None = None,
     split_k: int | None = None,
+    plan: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Decode one query row per request over the paged cache.
 
     ``query [R, Hq, D]``, caches ``[N, B, Hkv, D]`` (any strides with D
     contiguous), ``block_tables [R, W]`` and ``context_lens [R]`` on the device.
-    Returns ``[R, Hq, D]`` in the query dtype.
+    Returns ``[R, Hq, D]`` in the query dtype. ``plan`` is an optional
+    ``decode_plan(...)`` result for this step (same lengths, table width,
+    KV heads and split_k); without it the call computes its own.
     """
     if query.ndim != 3:
         raise ValueError("query must have shape [requests, Hq, D]")
@@ -152,10 +177,12 @@ def hip_paged_decode(
         )
     )
     stream = _lib.stream_handle(query.device)
-    workspace = counters = None
-    if ws_bytes:
-        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
-        counters = _decode_counters(query.device, stream, num_requests * num_kv_heads)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
+    counters = _decode_counters(query.device, stream, num_requests * num_kv_heads)
+    if plan is not None:
+        _lib.require_device(plan, what="hip_paged_decode")
+        if plan.dtype != torch.uint8 or not plan.is_contiguous():
+            raise ValueError("plan must come from decode_plan()")
     status = lib.mi_paged_decode(
         query.data_ptr(), query.stride(0), query.stride(1),
         key_cache.data_ptr(), value_cache.data_ptr(),
@@ -163,8 +190,8 @@ def hip_paged_decode(
         block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
         context_lens.data_ptr(),
         output.data_ptr(), output.stride(0), output.stride(1),
-        None if workspace is None else workspace.data_ptr(), ws_bytes,
-        None if counters is None else counters.data_ptr(),
+        workspace.data_ptr(), ws_bytes, counters.data_ptr(),
+        None if plan is None else plan.data_ptr(), 0 if plan is None else plan.numel(),
         num_requests, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
         split, float(scale), _lib.dtype_code(query.dtype), stream,
     )

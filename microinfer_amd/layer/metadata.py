@@ -36,6 +36,7 @@ class AttentionMetadata:
     _slot_block_size: int | None = field(default=None, repr=False)
     _slot_blocks: torch.Tensor | None = field(default=None, repr=False)
     _slot_offsets: torch.Tensor | None = field(default=None, repr=False)
+    _decode_plans: dict = field(default_factory=dict, repr=False)
 
     @classmethod
     def build(
@@ -88,6 +89,21 @@ class AttentionMetadata:
             self._slot_offsets = slots - blocks * block_size
             self._slot_block_size = block_size
         return self._slot_blocks, self._slot_offsets
+
+    def decode_plan(self, num_kv_heads: int, block_size: int) -> torch.Tensor:
+        """Device partition plan for this decode step, built once and reused
+        by every layer (like ``slot_indices``)."""
+        if self.context_lens is None or self.block_tables is None:
+            raise ValueError("decode plan needs context_lens and block_tables")
+        from microinfer_amd.layer.hip_paged_attention import decode_plan
+
+        key = (num_kv_heads, block_size, self.block_tables.shape[1])
+        plan = self._decode_plans.get(key)
+        if plan is None:
+            plan = decode_plan(self.context_lens, num_kv_heads=num_kv_heads,
+                               block_size=block_size, block_table_width=key[2])
+            self._decode_plans[key] = plan
+        return plan
 
     @property
     def cu_q_cpu(self) -> tuple[int, ...]:

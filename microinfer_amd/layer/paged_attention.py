@@ -74,6 +74,9 @@ def paged_attention_meta(
     if metadata.is_decode:
         if metadata.context_lens is None:
             raise RuntimeError("decode metadata requires context_lens")
+        plan = None
+        if metadata.context_lens.is_cuda:
+            plan = metadata.decode_plan(key_cache.shape[2], key_cache.shape[1])
         return hip_paged_decode(
             query,
             key_cache,
@@ -81,6 +84,7 @@ def paged_attention_meta(
             metadata.block_tables,
             metadata.context_lens,
             scale=scale,
+            plan=plan,
         )
 
     if metadata.cu_seqlens_q is None or metadata.cu_seqlens_k is None:

@@ -41,10 +41,10 @@ def test_invalid_arguments_fail_before_launch():
                               1, 1, 8, 16, 4, 9, None)
     assert status == 1 and "dtype" in _lib.last_error()
     status = lib.mi_paged_decode(None, 0, 0, None, None, 0, 0, 0, None, 0, 1, None, None, 0, 0,
-                                 None, 0, None, 1, 3, 2, 128, 16, 4, 0, 1.0, 2, None)
+                                 None, 0, None, None, 0, 1, 3, 2, 128, 16, 4, 0, 1.0, 2, None)
     assert status == 1 and "multiple" in _lib.last_error()
     status = lib.mi_paged_decode(None, 0, 0, None, None, 0, 0, 0, None, 0, 1, None, None, 0, 0,
-                                 None, 0, None, 1, 4, 2, 96, 16, 4, 0, 1.0, 2, None)
+                                 None, 0, None, None, 0, 1, 4, 2, 96, 16, 4, 0, 1.0, 2, None)
     assert status == 2 and "head_dim" in _lib.last_error()
     status = lib.mi_paged_prefill(None, 0, 0, None, None, 0, 0, 0, None, None, None, 0, 1,
                                   None, 0, 0, 4, 1, 4, 4, 2, 128, 12, 4, 1.0, 2, None)
@@ -59,7 +59,8 @@ def test_empty_work_is_a_no_op():
     assert lib.mi_kv_append(None, 0, 0, None, 0, 0, None, None, 0, 0, 0, None, None, 0,
                             0, 8, 128, 16, 4, 2, None) == 0
     assert lib.mi_paged_decode(None, 0, 0, None, None, 0, 0, 0, None, 0, 1, None, None, 0, 0,
-                               None, 0, None, 0, 16, 8, 128, 16, 4, 0, 1.0, 2, None) == 0
+                               None, 0, None, None, 0, 0, 16, 8, 128, 16, 4, 0, 1.0, 2,
+                               None) == 0
 
 
 def test_missing_workspace_is_reported():
@@ -68,22 +69,38 @@ def test_missing_workspace_is_reported():
     assert need > 0
     fake = ctypes.c_void_p(256)
     status = lib.mi_paged_decode(fake, 2048, 128, fake, fake, 16384, 1024, 128, fake, 128, 128,
-                                 fake, fake, 2048, 128, None, 0, None, 32, 16, 8, 128, 16, 4096,
-                                 0, 1.0, 2, None)
+                                 fake, fake, 2048, 128, None, 0, None, None, 0, 32, 16, 8, 128,
+                                 16, 4096, 0, 1.0, 2, None)
     assert status == 3 and "workspace" in _lib.last_error()
     status = lib.mi_paged_decode(fake, 2048, 128, fake, fake, 16384, 1024, 128, fake, 128, 128,
-                                 fake, fake, 2048, 128, fake, need, None, 32, 16, 8, 128, 16,
-                                 4096, 0, 1.0, 2, None)
+                                 fake, fake, 2048, 128, fake, need, None, None, 0, 32, 16, 8, 128,
+                                 16, 4096, 0, 1.0, 2, None)
     assert status == 3 and "counters" in _lib.last_error()
+    # A plan buffer smaller than the current tuning needs is refused.
+    status = lib.mi_paged_decode(fake, 2048, 128, fake, fake, 16384, 1024, 128, fake, 128, 128,
+                                 fake, fake, 2048, 128, fake, need, fake, fake, 64, 32, 16, 8,
+                                 128, 16, 4096, 0, 1.0, 2, None)
+    assert status == 1 and "plan" in _lib.last_error()
 
 
-@pytest.mark.parametrize("split_k,expect_zero", [(1, True), (0, False), (4, False)])
-def test_workspace_size_formula(split_k, expect_zero):
+def test_decode_plan_validation_and_size():
+    lib = _lib.load()
+    assert lib.mi_decode_plan_bytes(32, 8, 0) == (512 // 8 + 32) * 32
+    assert lib.mi_decode_plan_bytes(4, 8, 16) == 4 * 16 * 32
+    fake = ctypes.c_void_p(256)
+    assert lib.mi_decode_plan(fake, 32, 8, 12, 128, 0, fake, 10 ** 6, None) == 1
+    assert "block_size" in _lib.last_error()
+    assert lib.mi_decode_plan(fake, 5000, 8, 16, 128, 0, fake, 10 ** 6, None) == 2
+    assert lib.mi_decode_plan(fake, 32, 8, 16, 128, 0, fake, 64, None) == 3
+    assert lib.mi_decode_plan(None, 0, 8, 16, 128, 0, None, 0, None) == 0
+
+
+@pytest.mark.parametrize("split_k", [1, 0, 4])
+def test_workspace_size_formula(split_k):
     lib = _lib.load()
     size = lib.mi_paged_decode_workspace_bytes(4, 32, 8, 128, split_k)
-    if expect_zero:
-        assert size == 0
-    elif split_k:
-        assert size == 4 * split_k * 8 * 4 * (128 + 2) * 4
-    else:
-        assert size % (8 * 4 * 130 * 4) == 0
+    plan = lib.mi_decode_plan_bytes(4, 8, split_k)
+    plan_region = (plan + 255) // 256 * 256
+    items = plan // 32
+    partials = 0 if split_k == 1 else items * 8 * 4 * (128 + 2) * 4
+    assert size == plan_region + partials

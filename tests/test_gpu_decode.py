@@ -245,6 +245,28 @@ def test_split_counters_are_left_zeroed():
     assert max_abs(first, expected) <= 2e-2 and max_abs(third, expected) <= 2e-2
 
 
+@pytest.mark.parametrize("split_k", [None, 1, 4])
+def test_shared_step_plan_matches_per_call_plan(split_k):
+    from microinfer_amd.layer.hip_paged_attention import decode_plan
+
+    torch.manual_seed(7)
+    kc = torch.randn(2048, 16, 8, 128, device=DEV).to(torch.bfloat16)
+    vc = torch.randn_like(kc)
+    batch = make_decode_batch(num_seqs=24, ctx_lo=1, ctx_hi=1500, pool_blocks=2048,
+                              draw_pools=False, **QWEN3_06B)
+    tables = torch.tensor(batch.block_tables, device=DEV)
+    lens = torch.tensor(batch.context_lens, device=DEV)
+    plan = decode_plan(lens, num_kv_heads=8, block_size=16, block_table_width=tables.shape[1],
+                       split_k=split_k)
+    for layer in range(3):
+        q = torch.randn(24, 16, 128, device=DEV).to(torch.bfloat16)
+        own = hip_paged_decode(q, kc, vc, tables, lens, split_k=split_k)
+        shared = hip_paged_decode(q, kc, vc, tables, lens, split_k=split_k, plan=plan)
+        assert torch.equal(own, shared), f"layer {layer}"
+    expected = oracle_decode(q, kc, vc, tables, lens, 1 / math.sqrt(128))
+    assert max_abs(shared, expected) <= 2e-2
+
+
 def test_hipgraph_replay_tracks_new_contexts():
     torch.manual_seed(5)
     kc = torch.randn(512, 16, 8, 128, device=DEV).to(torch.bfloat16)
