@@ -3,14 +3,15 @@
 
 Workload (one "step"): the decode attention of a random-init Qwen3-0.6B layer
 stack -- 16 Q / 8 KV heads, head_dim 128, bf16, block 16 -- for 32 sequences
-with contexts U[128, 2048] over a 16384-block pool per layer. A step is 28
-independent layer calls, each one KV append of the 32 new rows plus paged
-decode attention over that layer's own cache (28 distinct 1.07 GB caches, so
-nothing is served from the 256 MB last-level cache). The step is captured in
-a hipGraph and replayed; inputs are resident in HBM before timing.
+with contexts U[128, 2048] over a 16384-block pool per layer. A step is one
+partition plan plus 28 independent layer calls, each one launch that appends
+the 32 new K/V rows and runs paged decode attention over that layer's own
+cache (28 distinct 1.07 GB caches, so nothing is served from the 256 MB
+last-level cache). The step is captured in a hipGraph and replayed; inputs
+are resident in HBM before timing.
 
 Prints one JSON line: value = whole-step algorithmic HBM bytes / step time
-(GB/s), the roofline of the decode layer call and a CPU-oracle baseline.
+(GB/s), the roofline of the decode launch and a CPU-oracle baseline.
 """
 
 from __future__ import annotations
@@ -86,6 +87,15 @@ def build_decode_state(torch, layers: int, layout: str):
     )
 
 
+def copy_calibration(torch, mib: int) -> None:
+    """One plain device-to-device copy of ``mib`` MiB (reads and writes that many)."""
+    src = torch.empty(mib << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"calibration copy of {mib} MiB done")
+
+
 def cpu_baseline(torch, state, samples: int = 5):
     """Oracle (numpy restatement of the reference CPU path) on layer 0's call."""
     from microinfer_amd.workloads import decode_bytes
@@ -147,6 +157,11 @@ def main() -> int:
     parser.add_argument("--layers", type=int, default=28)
     parser.add_argument("--layout", default="head_major", choices=["head_major", "token_major"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-graph", action="store_true",
+                        help="launch the step eagerly (for per-dispatch counter runs)")
+    parser.add_argument("--copy-calibration-mib", type=int, default=0,
+                        help="after timing, run one device copy of this many MiB (the "
+                             "known-size kernel that scales FETCH_SIZE / WRITE_SIZE)")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -162,43 +177,52 @@ def main() -> int:
 
     log("allocating 28-layer caches")
     state = build_decode_state(torch, args.layers, args.layout)
-    views, query, tables, lens, slots = (state[k] for k in ("views", "query", "tables", "lens", "slots"))
+    views, query, tables, lens = (state[k] for k in ("views", "query", "tables", "lens"))
     new_k, new_v = state["new_k"], state["new_v"]
     scale = 1 / math.sqrt(128)
     outputs = []
 
     def step():
         # One partition plan per step, shared by the 28 layers (as the
-        # engine's AttentionMetadata does).
+        # engine's AttentionMetadata does); each layer call appends its new
+        # rows and attends in one launch.
         plan = decode_plan(lens, num_kv_heads=8, block_size=16,
                            block_table_width=tables.shape[1])
         outputs.clear()
         for layer, view in enumerate(views):
-            view.write_slots(slots, new_k[layer], new_v[layer])
             outputs.append(hip_paged_decode(query[layer], view.keys, view.values, tables, lens,
-                                            scale=scale, plan=plan))
+                                            scale=scale, plan=plan, new_keys=new_k[layer],
+                                            new_values=new_v[layer]))
 
     step()
     torch.cuda.synchronize()
-    log("capturing the decode step in a hipGraph")
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
-    torch.cuda.synchronize()
+    if args.no_graph:
+        run = step
+    else:
+        log("capturing the decode step in a hipGraph")
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+        run = graph.replay
 
     for _ in range(args.warmup):
-        graph.replay()
+        run()
     torch.cuda.synchronize()
+    # Events on torch's current stream, which is the stream every launch of
+    # the step goes to (the library reads it at call time).
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     log(f"timing {args.steps} steps")
     t0 = time.perf_counter()
     start.record()
     for _ in range(args.steps):
-        graph.replay()
+        run()
     end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = start.elapsed_time(end) / args.steps
+    if args.copy_calibration_mib:
+        copy_calibration(torch, args.copy_calibration_mib)
 
     contexts = state["batch"].context_lens
     layer_bytes = decode_bytes(contexts, num_q_heads=16, num_kv_heads=8, head_dim=128,
@@ -240,9 +264,11 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "decode layer call (append + paged decode + split merge)",
+            "kernel": "paged_attention_vector_kernel (fused append + decode + split merge)",
             "bytes_per_launch": layer_bytes,
             "us_per_launch": round(layer_us, 3),
+            "timing": "HIP events around the timed steps / (steps x layers); includes the "
+                      "per-step plan kernel and inter-launch gaps",
         },
     }
     if not args.no_cpu_baseline:

@@ -151,6 +151,44 @@ int32_t mi_paged_decode(const void* query, int64_t q_token_stride, int64_t q_hea
                         float scale, int32_t dtype, void* stream);
 
 /*
+ * Decode step of one layer with the KV append fused in: for every sequence s
+ * with context_lens[s] = c >= 1, row s of new_keys / new_values ([num_seqs,
+ * Hkv, D], token and head strides in elements) is written to cache position
+ * c - 1 (block block_tables[s][(c-1)/B], offset (c-1)%B), and the attention
+ * over positions 0..c-1 includes it. Same result as mi_kv_append with
+ * slot_mapping[s] = block_tables[s][(c-1)/B]*B + (c-1)%B followed by
+ * mi_paged_decode, in one launch, with the new row read once.
+ *
+ * Replaces, for decode steps, CachedAttention.forward's append-then-attend
+ * (microinfer/layer/cached_attention.py:76-85: LayerKVCache.write_fast,
+ * microinfer/worker/kv_cache.py:52-79, then paged_attention_meta); the runner
+ * builds slot_mapping exactly this way (microinfer/runner.py:167-174).
+ * A position whose block id is negative or >= num_blocks is neither written
+ * nor attended (the append skips it and the attention masks it). Sequences
+ * whose plan context differs from context_lens are not appended. The block
+ * that receives a sequence's new row must not be read by another sequence of
+ * the same call (its read would race with the write); the reference's block
+ * manager guarantees this, as only full blocks are ever shared
+ * (microinfer/engine/blockmanager.py:144-174). All other arguments and rules
+ * are those of mi_paged_decode.
+ */
+int32_t mi_paged_decode_append(const void* new_keys, int64_t nk_token_stride,
+                               int64_t nk_head_stride, const void* new_values,
+                               int64_t nv_token_stride, int64_t nv_head_stride,
+                               const void* query, int64_t q_token_stride,
+                               int64_t q_head_stride, void* key_cache, void* value_cache,
+                               int64_t cache_block_stride, int64_t cache_token_stride,
+                               int64_t cache_head_stride, const int32_t* block_tables,
+                               int64_t block_table_stride, int32_t block_table_width,
+                               const int32_t* context_lens, void* out,
+                               int64_t out_token_stride, int64_t out_head_stride,
+                               void* workspace, int64_t workspace_bytes, int32_t* counters,
+                               const void* plan, int64_t plan_bytes, int32_t num_seqs,
+                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                               int32_t block_size, int32_t num_blocks, int32_t split_k,
+                               float scale, int32_t dtype, void* stream);
+
+/*
  * Paged varlen (prefill / mixed) attention with a bottom-right causal mask:
  * request r owns query rows [cu_seqlens_q[r], cu_seqlens_q[r+1]) and context
  * c_r = cu_seqlens_k[r+1] - cu_seqlens_k[r]; its query row i sits at position

@@ -41,6 +41,12 @@ SIGNATURES = {
         [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P, _P, _I64, _I64,
          _P, _I64, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P],
     ),
+    "mi_paged_decode_append": (
+        _I32,
+        [_P, _I64, _I64, _P, _I64, _I64,
+         _P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P, _P, _I64, _I64,
+         _P, _I64, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P],
+    ),
     "mi_decode_plan_bytes": (_I64, [_I32, _I32, _I32]),
     "mi_decode_plan": (_I32, [_P, _I32, _I32, _I32, _I32, _I32, _P, _I64, _P]),
     "mi_paged_prefill": (

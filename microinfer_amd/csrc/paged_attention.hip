@@ -70,18 +70,27 @@ extern "C" int64_t mi_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num
              static_cast<int64_t>(sizeof(float));
 }
 
-extern "C" int32_t mi_paged_decode(
+namespace mi {
+namespace {
+
+// The step's new K/V rows for the fused append (all null: no append).
+struct NewRows {
+  const void* keys = nullptr;
+  int64_t k_ts = 0, k_hs = 0;
+  const void* values = nullptr;
+  int64_t v_ts = 0, v_hs = 0;
+};
+
+int32_t paged_decode(
     const void* query, int64_t q_token_stride, int64_t q_head_stride, const void* key_cache,
     const void* value_cache, int64_t cache_block_stride, int64_t cache_token_stride,
     int64_t cache_head_stride, const int32_t* block_tables, int64_t block_table_stride,
     int32_t block_table_width, const int32_t* context_lens, void* out,
     int64_t out_token_stride, int64_t out_head_stride, void* workspace,
     int64_t workspace_bytes, int32_t* counters, const void* plan, int64_t plan_bytes,
-    int32_t num_seqs,
-    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-    int32_t num_blocks, int32_t split_k, float scale, int32_t dtype, void* stream) {
-  using namespace mi;
-  clear_error();
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t block_size, int32_t num_blocks, int32_t split_k, float scale, int32_t dtype,
+    const NewRows& rows, void* stream) {
   int32_t st = check_common("mi_paged_decode", dtype, num_q_heads, num_kv_heads, head_dim,
                             block_size, num_blocks, block_table_width);
   if (st != MI_OK) return st;
@@ -100,6 +109,13 @@ extern "C" int32_t mi_paged_decode(
       cache_block_stride % vec || cache_token_stride % vec || cache_head_stride % vec ||
       out_token_stride % vec || out_head_stride % vec)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode: misaligned pointers or strides");
+  if ((rows.keys == nullptr) != (rows.values == nullptr))
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_append: null new keys or values");
+  if (rows.keys != nullptr &&
+      (!aligned(rows.keys, vb) || !aligned(rows.values, vb) || rows.k_ts % vec ||
+       rows.k_hs % vec || rows.v_ts % vec || rows.v_hs % vec))
+    return fail(MI_ERR_INVALID_ARGUMENT,
+                "mi_paged_decode_append: misaligned new-row pointers or strides");
   const int64_t need = mi_paged_decode_workspace_bytes(num_seqs, num_q_heads, num_kv_heads,
                                                        head_dim, split_k);
   if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 256))
@@ -142,6 +158,12 @@ extern "C" int32_t mi_paged_decode(
   a.max_items = decode_max_items(num_seqs, num_kv_heads, split_k);
   a.scale_log2 = scale * kLog2e;
   a.varlen = 0;
+  a.new_k = rows.keys;
+  a.nk_ts = rows.k_ts;
+  a.nk_hs = rows.k_hs;
+  a.new_v = rows.values;
+  a.nv_ts = rows.v_ts;
+  a.nv_hs = rows.v_hs;
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   const int64_t plan_region = round_up(decode_plan_bytes(num_seqs, num_kv_heads, split_k), 256);
@@ -162,6 +184,60 @@ extern "C" int32_t mi_paged_decode(
     a.counters = counters;
   }
   return dispatch_vector(a, dtype, s);
+}
+
+}  // namespace
+}  // namespace mi
+
+extern "C" int32_t mi_paged_decode(
+    const void* query, int64_t q_token_stride, int64_t q_head_stride, const void* key_cache,
+    const void* value_cache, int64_t cache_block_stride, int64_t cache_token_stride,
+    int64_t cache_head_stride, const int32_t* block_tables, int64_t block_table_stride,
+    int32_t block_table_width, const int32_t* context_lens, void* out,
+    int64_t out_token_stride, int64_t out_head_stride, void* workspace,
+    int64_t workspace_bytes, int32_t* counters, const void* plan, int64_t plan_bytes,
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t block_size, int32_t num_blocks, int32_t split_k, float scale, int32_t dtype,
+    void* stream) {
+  mi::clear_error();
+  return mi::paged_decode(query, q_token_stride, q_head_stride, key_cache, value_cache,
+                          cache_block_stride, cache_token_stride, cache_head_stride,
+                          block_tables, block_table_stride, block_table_width, context_lens,
+                          out, out_token_stride, out_head_stride, workspace, workspace_bytes,
+                          counters, plan, plan_bytes, num_seqs, num_q_heads, num_kv_heads,
+                          head_dim, block_size, num_blocks, split_k, scale, dtype,
+                          mi::NewRows{}, stream);
+}
+
+extern "C" int32_t mi_paged_decode_append(
+    const void* new_keys, int64_t nk_token_stride, int64_t nk_head_stride,
+    const void* new_values, int64_t nv_token_stride, int64_t nv_head_stride,
+    const void* query, int64_t q_token_stride, int64_t q_head_stride, void* key_cache,
+    void* value_cache, int64_t cache_block_stride, int64_t cache_token_stride,
+    int64_t cache_head_stride, const int32_t* block_tables, int64_t block_table_stride,
+    int32_t block_table_width, const int32_t* context_lens, void* out,
+    int64_t out_token_stride, int64_t out_head_stride, void* workspace,
+    int64_t workspace_bytes, int32_t* counters, const void* plan, int64_t plan_bytes,
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t block_size, int32_t num_blocks, int32_t split_k, float scale, int32_t dtype,
+    void* stream) {
+  mi::clear_error();
+  if (new_keys == nullptr || new_values == nullptr)
+    return mi::fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_append: null new keys or values");
+  mi::NewRows rows;
+  rows.keys = new_keys;
+  rows.k_ts = nk_token_stride;
+  rows.k_hs = nk_head_stride;
+  rows.values = new_values;
+  rows.v_ts = nv_token_stride;
+  rows.v_hs = nv_head_stride;
+  return mi::paged_decode(query, q_token_stride, q_head_stride, key_cache, value_cache,
+                          cache_block_stride, cache_token_stride, cache_head_stride,
+                          block_tables, block_table_stride, block_table_width, context_lens,
+                          out, out_token_stride, out_head_stride, workspace, workspace_bytes,
+                          counters, plan, plan_bytes, num_seqs, num_q_heads, num_kv_heads,
+                          head_dim, block_size, num_blocks, split_k, scale, dtype, rows,
+                          stream);
 }
 
 extern "C" int32_t mi_paged_prefill(

@@ -94,6 +94,28 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
     first_item = it.first_item;
   }
 
+  // Fused append (decode): the partition holding position ctx - 1 owns the
+  // step's new K/V row of (seq, head). Its wave 0 stores the row into the
+  // cache and attends to it from registers, so no load of that position is
+  // ordered after the store. A sequence whose plan context disagrees with
+  // context_lens (stale plan, or a context past the table) is not appended.
+  bool append = false;
+  int64_t append_off = -1;  // element offset of the cache row; -1: no valid block
+  Pack<R, VEC> new_kp, new_vp;
+  if (!a.varlen && a.new_k != nullptr && ctx >= 1) {
+    const int last = (ctx - 1) >> a.log2_block;
+    append = blk_begin <= last && last < blk_end && a.ctx[seq] == ctx;
+    if (append && wave == 0) {
+      const int blk = a.tables[seq * a.t_stride + last];
+      if (blk >= 0 && blk < a.num_blocks)
+        append_off = blk * a.c_bs + ((ctx - 1) & (a.block_size - 1)) * a.c_ts + head * a.c_hs;
+      new_kp = load_pack<R, VEC>(static_cast<const R*>(a.new_k) + seq * a.nk_ts +
+                                 head * a.nk_hs + d0);
+      new_vp = load_pack<R, VEC>(static_cast<const R*>(a.new_v) + seq * a.nv_ts +
+                                 head * a.nv_hs + d0);
+    }
+  }
+
   // Query rows of the G heads. 16-bit types keep raw element pairs for the
   // packed dot2 instructions; scores are scaled into the log2 domain after
   // the row sum.
@@ -139,7 +161,7 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
   int pos_begin, pos_end;
   if (paged) {
     pos_begin = blk_begin << lb;
-    pos_end = min(ctx, blk_end << lb);
+    pos_end = min(append ? ctx - 1 : ctx, blk_end << lb);
   } else {
     pos_begin = 0;
     pos_end = static_cast<int>(min<int64_t>(ctx, max<int64_t>(a.num_blocks - row0, 0)));
@@ -260,6 +282,40 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
       consume(B);
       if (t2 >= pos_end) break;
       t0 = t2;
+    }
+  }
+
+  // The appended row: wave 0 stores it into the cache (lane group 0) and
+  // folds it into lane group 0's softmax state. A row whose block id is
+  // invalid is neither stored nor attended, as a skipped append would leave
+  // that position masked.
+  if (append && wave == 0) {
+    const bool ok = grp == 0 && append_off >= 0;
+    if (ok) {
+      store_pack<R, VEC>(const_cast<R*>(kc) + append_off + d0, new_kp);
+      store_pack<R, VEC>(const_cast<R*>(vc) + append_off + d0, new_vp);
+    }
+    const Pack<QWord, QW> kw = __builtin_bit_cast(Pack<QWord, QW>, new_kp);
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      float dot = 0.f;
+#pragma unroll
+      for (int j = 0; j < QW; ++j) {
+        if constexpr (PAIRS) {
+          dot = E::dot2(qv[g][j], kw.v[j], dot);
+        } else {
+          dot = fmaf(qv[g][j], kw.v[j], dot);
+        }
+      }
+      dot = group_sum<LPR>(dot) * scale_log2;
+      if (!ok || (!EXACT && g >= G)) continue;
+      const float mnew = fmaxf(m[g], dot);
+      const float alpha = (m[g] == -INFINITY) ? 0.f : fast_exp2(m[g] - mnew);
+      const float p = fast_exp2(dot - mnew);
+      m[g] = mnew;
+      lsum[g] = fmaf(lsum[g], alpha, p);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) acc[g][j] = fmaf(acc[g][j], alpha, p * E::load(new_vp.v[j]));
     }
   }
 

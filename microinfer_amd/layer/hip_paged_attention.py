@@ -122,6 +122,8 @@ def hip_paged_decode(
     scale: float | None = None,
     split_k: int | None = None,
     plan: torch.Tensor | None = None,
+    new_keys: torch.Tensor | None = None,
+    new_values: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Decode one query row per request over the paged cache.
 
@@ -130,6 +132,13 @@ def hip_paged_decode(
     Returns ``[R, Hq, D]`` in the query dtype. ``plan`` is an optional
     ``decode_plan(...)`` result for this step (same lengths, table width,
     KV heads and split_k); without it the call computes its own.
+
+    ``new_keys`` / ``new_values`` (``[R, Hkv, D]``) fuse the step's KV append
+    into the launch: row r is stored at cache position ``context_lens[r] - 1``
+    (the slot the runner assigns a decode token, microinfer/runner.py:167-174)
+    before it is attended, as CachedAttention.forward's append-then-attend
+    does (microinfer/layer/cached_attention.py:76-85). The caches are then
+    written in place and must share strides.
     """
     if query.ndim != 3:
         raise ValueError("query must have shape [requests, Hq, D]")
@@ -161,6 +170,21 @@ def hip_paged_decode(
         raise ValueError("context_lens must have one entry per request")
     _lib.require_device(block_tables, context_lens, what="hip_paged_decode")
 
+    append = new_keys is not None or new_values is not None
+    if append:
+        if new_keys is None or new_values is None:
+            raise ValueError("new_keys and new_values must be given together")
+        for name, rows in (("new_keys", new_keys), ("new_values", new_values)):
+            if rows.shape != (num_requests, num_kv_heads, head_dim):
+                raise ValueError(f"{name} must have shape [requests, Hkv, D]")
+            if rows.dtype != query.dtype or rows.device != query.device:
+                raise ValueError(f"{name} must share the query's dtype and device")
+        if (key_cache.stride(-1) != 1 or value_cache.stride(-1) != 1
+                or key_cache.stride() != value_cache.stride()):
+            raise ValueError("an appending decode writes the caches in place: they need "
+                             "equal strides with a contiguous head_dim")
+        new_keys = _inner_contiguous(new_keys)
+        new_values = _inner_contiguous(new_values)
     key_cache, value_cache = _check_caches(key_cache, value_cache)
     query = _inner_contiguous(query)
     block_tables = _index32(block_tables)
@@ -183,7 +207,7 @@ def hip_paged_decode(
         _lib.require_device(plan, what="hip_paged_decode")
         if plan.dtype != torch.uint8 or not plan.is_contiguous():
             raise ValueError("plan must come from decode_plan()")
-    status = lib.mi_paged_decode(
+    args = (
         query.data_ptr(), query.stride(0), query.stride(1),
         key_cache.data_ptr(), value_cache.data_ptr(),
         key_cache.stride(0), key_cache.stride(1), key_cache.stride(2),
@@ -195,7 +219,14 @@ def hip_paged_decode(
         num_requests, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
         split, float(scale), _lib.dtype_code(query.dtype), stream,
     )
-    _lib.check(status, "mi_paged_decode")
+    if append:
+        status = lib.mi_paged_decode_append(
+            new_keys.data_ptr(), new_keys.stride(0), new_keys.stride(1),
+            new_values.data_ptr(), new_values.stride(0), new_values.stride(1), *args)
+        _lib.check(status, "mi_paged_decode_append")
+    else:
+        status = lib.mi_paged_decode(*args)
+        _lib.check(status, "mi_paged_decode")
     return output
 
 
