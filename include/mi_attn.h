@@ -133,7 +133,7 @@ int32_t mi_decode_plan(const int32_t* context_lens, int32_t num_seqs, int32_t nu
  * target_items (work item, KV head) workgroups per launch, each covering at
  * least min_part_blocks cache blocks. Values <= 0 leave a knob unchanged.
  * Process-wide; changes the size mi_paged_decode_workspace_bytes reports, so
- * set it before sizing workspaces or capturing graphs. Defaults 512 / 4.
+ * set it before sizing workspaces or capturing graphs. Defaults 192 / 4.
  */
 void mi_tune_decode(int32_t target_items, int32_t min_part_blocks);
 

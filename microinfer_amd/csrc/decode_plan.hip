@@ -14,7 +14,7 @@
 namespace mi {
 namespace {
 
-int32_t g_target_items = 512;
+int32_t g_target_items = 192;
 int32_t g_min_part_blocks = 4;
 
 constexpr int kPlanThreads = 1024;

@@ -512,7 +512,7 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
 #define MI_TILE_UNROLL_LARGE_GROUP 4
 #endif
 #ifndef MI_WAVES_PER_GROUP
-#define MI_WAVES_PER_GROUP 4
+#define MI_WAVES_PER_GROUP 8
 #endif
 // Waves per workgroup: they split one partition and merge through LDS.
 constexpr int kWavesPerGroup = MI_WAVES_PER_GROUP;

@@ -85,7 +85,7 @@ def test_missing_workspace_is_reported():
 
 def test_decode_plan_validation_and_size():
     lib = _lib.load()
-    assert lib.mi_decode_plan_bytes(32, 8, 0) == (512 // 8 + 32) * 32
+    assert lib.mi_decode_plan_bytes(32, 8, 0) == (192 // 8 + 32) * 32
     assert lib.mi_decode_plan_bytes(4, 8, 16) == 4 * 16 * 32
     fake = ctypes.c_void_p(256)
     assert lib.mi_decode_plan(fake, 32, 8, 12, 128, 0, fake, 10 ** 6, None) == 1
