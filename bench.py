@@ -149,6 +149,136 @@ def cpu_baseline(torch, state, samples: int = 5):
     }
 
 
+def prefill_cpu_baseline(torch, batch, q, cache, samples: int = 3):
+    """Oracle on a bounded sample of the mixed batch: 2 prefill chunks + the decode rows."""
+    from microinfer_amd.workloads import prefill_flops
+    from oracle import paged_attention_reference
+
+    rows = [0, 1] + list(range(8, len(batch.q_lens)))
+    tables = batch.block_tables[rows]
+    contexts = [int(batch.context_lens[r]) for r in rows]
+    used = sorted({int(b) for i, c in enumerate(contexts) for b in tables[i, : (c + 15) // 16]})
+    remap = {b: i for i, b in enumerate(used)}
+    small = np.full_like(tables, -1)
+    for i, c in enumerate(contexts):
+        for j in range((c + 15) // 16):
+            small[i, j] = remap[int(tables[i, j])]
+    index = torch.tensor(used, dtype=torch.long, device=cache.keys[0].device)
+    host_k = cache.keys[0].index_select(0, index).float().cpu().numpy()
+    host_v = cache.values[0].index_select(0, index).float().cpu().numpy()
+    q_rows = np.concatenate([np.arange(batch.cu_seqlens_q[r], batch.cu_seqlens_q[r + 1]) for r in rows])
+    host_q = q[torch.tensor(q_rows, device=q.device)].float().cpu().numpy()
+    q_lens = [int(batch.q_lens[r]) for r in rows]
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).tolist()
+    scale = 1 / math.sqrt(128)
+    paged_attention_reference(host_q, host_k, host_v, small, contexts, cu, scale=scale)
+    times = []
+    for _ in range(samples):
+        t0 = time.perf_counter()
+        paged_attention_reference(host_q, host_k, host_v, small, contexts, cu, scale=scale)
+        times.append(time.perf_counter() - t0)
+    per_call = statistics.median(times)
+    flops = prefill_flops(q_lens, contexts, num_q_heads=32, head_dim=128)
+    return {
+        "value": round(flops / per_call / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": blas_threads(),
+        "kind": "port",
+        "sample": (f"2 of the 8 prefill chunks + the 24 decode rows ({flops / 1e9:.1f} GFLOP), "
+                   f"x {samples} runs after 1 warm-up, median {per_call * 1e3:.0f} ms; "
+                   f"numpy/BLAS on {os.cpu_count()} host CPUs ({cpu_model()})"),
+    }
+
+
+def run_prefill(args) -> int:
+    """Mixed chunked prefill (8B shape): one varlen launch per step."""
+    import torch
+
+    from microinfer_amd.layer.hip_paged_attention import hip_paged_prefill
+    from microinfer_amd.workloads import make_mixed_prefill_batch, prefill_flops
+    from microinfer_amd.worker.kv_cache import KVCache
+
+    batch = make_mixed_prefill_batch()
+    dev = torch.device("cuda", 0)
+    log("allocating the 8B-shape cache (65536 blocks)")
+    cache = KVCache(1, batch.pool_blocks, 16, 8, 128, dtype=torch.bfloat16, device=dev,
+                    layout=args.layout)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    cache.keys[0].copy_(torch.randn(cache.keys[0].shape, generator=gen, device=dev))
+    cache.values[0].copy_(torch.randn(cache.values[0].shape, generator=gen, device=dev))
+    total_q = int(batch.q_lens.sum())
+    q = torch.randn((total_q, 32, 128), generator=gen, device=dev).to(torch.bfloat16)
+    tables = torch.tensor(batch.block_tables, device=dev)
+    cu_q = torch.tensor(batch.cu_seqlens_q, device=dev)
+    cu_k = torch.tensor(batch.cu_seqlens_k, device=dev)
+    max_q = int(batch.q_lens.max())
+    scale = 1 / math.sqrt(128)
+    out = torch.empty_like(q)
+
+    def step():
+        out.copy_(hip_paged_prefill(q, cache.keys[0], cache.values[0], cu_q, cu_k, tables,
+                                    max_seqlen_q=max_q, scale=scale))
+
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    flops = prefill_flops(batch.q_lens, batch.context_lens, num_q_heads=32, head_dim=128)
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"{ms * 1e3:.1f} us per launch, {tflops:.1f} TFLOP/s")
+    result = {
+        "metric": "paged chunked-prefill attention TFLOP/s (% of bf16 dense MFMA peak)",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) Q/K/V, random block tables with shared prefix blocks",
+        "config": {
+            "workload": ("mixed chunked prefill, Qwen3-8B attention (32 Q / 8 KV heads, "
+                         "head_dim 128), bf16, block 16, pool 65536 blocks: 8 chunks of 512 "
+                         "rows on prefixes U[0,3072] (first 1024 tokens shared) + 24 decode "
+                         "rows with contexts U[256,2048] (seed 0), one varlen launch, hipGraph "
+                         "replay"),
+            "query_rows": total_q,
+            "flops_per_launch": flops,
+            "kv_layout": args.layout,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops, 2),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "kernel": "paged_prefill_mfma_kernel",
+            "flops_per_launch": flops,
+            "us_per_launch": round(ms * 1e3, 3),
+        },
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle on a sample of the batch")
+        result["cpu_baseline"] = prefill_cpu_baseline(torch, batch, q, cache)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -157,6 +287,9 @@ def main() -> int:
     parser.add_argument("--layers", type=int, default=28)
     parser.add_argument("--layout", default="head_major", choices=["head_major", "token_major"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--workload", default="decode", choices=["decode", "prefill"],
+                        help="decode: the headline paged-decode line; prefill: the mixed "
+                             "chunked-prefill (MFMA) line")
     parser.add_argument("--no-graph", action="store_true",
                         help="launch the step eagerly (for per-dispatch counter runs)")
     parser.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -169,9 +302,12 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    if args.workload == "prefill":
+        return run_prefill(args)
+
     import torch
 
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from microinfer_amd.layer.hip_paged_attention import decode_plan, hip_paged_decode
     from microinfer_amd.workloads import decode_bytes
 

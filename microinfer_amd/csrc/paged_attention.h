@@ -53,6 +53,11 @@ struct AttnArgs {
 int32_t launch_paged_attention_vector(const AttnArgs& args, int32_t dtype,
                                       hipStream_t stream);
 
+// MFMA varlen (prefill) kernel (paged_prefill_mfma.hip): whether it takes
+// this call, and its launch.
+bool prefill_mfma_supported(const AttnArgs& args, int32_t dtype);
+int32_t launch_prefill_mfma(const AttnArgs& args, int32_t dtype, hipStream_t stream);
+
 // Upper bound on decode work items for a launch (grid.x / Hkv).
 int32_t decode_max_items(int32_t num_seqs, int32_t num_kv_heads, int32_t split_k);
 

@@ -298,5 +298,9 @@ extern "C" int32_t mi_paged_prefill(
   a.num_blocks = num_blocks;
   a.scale_log2 = scale * kLog2e;
   a.varlen = 1;
+  // bf16/f16 with head_dim 128 and GQA groups 1, 2, 4 run on MFMA; every
+  // other supported shape on the vector kernel.
+  if (prefill_mfma_supported(a, dtype))
+    return launch_prefill_mfma(a, dtype, static_cast<hipStream_t>(stream));
   return dispatch_vector(a, dtype, static_cast<hipStream_t>(stream));
 }

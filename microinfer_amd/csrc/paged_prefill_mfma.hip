@@ -1,0 +1,319 @@
+// Paged varlen (chunked prefill / mixed) attention on bf16/f16 MFMA, gfx950.
+//
+// Replaces _paged_prefill_kernel (microinfer/layer/triton_paged_attention.py:
+// 134-233): causal attention of each request's query rows over its paged
+// context with the bottom-right alignment q_pos = (c - q_len) + i
+// (microinfer/layer/paged_attention.py:57-62).
+//
+// Design (head_dim 128, G = Hq/Hkv in {1, 2, 4}, block size >= 16):
+//  * Workgroup = (request, block of BM query rows, KV head) with all G query
+//    heads of the KV head: 4 waves, wave w takes query head w % G and 32 rows,
+//    so a K/V tile staged in LDS serves G heads.
+//  * Per 32-key tile, S^T = K . Q^T on v_mfma_f32_32x32x16 (A = K rows from
+//    LDS, B = Q^T held in registers for the whole kernel). In the result each
+//    lane owns one query row's 16 keys (the other 16 sit in lane ^ 32), so the
+//    online softmax needs one cross-lane exchange per statistic.
+//  * O^T += V^T . P^T on the same instruction: P^T comes straight from the
+//    softmax registers. The MFMA reduction index is mapped to keys the way
+//    the S^T result lays them out, and V is stored transposed in LDS with the
+//    same mapping, so no shuffles of P are needed.
+//  * K/V tiles are double-buffered in LDS; the next tile's global loads are in
+//    flight while the current tile is computed. One barrier per tile.
+#include "paged_attention.h"
+
+namespace mi {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// Probability (in [0, 1]) to the raw 16-bit element; gfx950 converts to
+// bf16 with round-to-nearest-even in hardware.
+template <typename E>
+__device__ __forceinline__ uint16_t to_raw(float x) {
+  if constexpr (std::is_same<E, BF16>::value) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
+  } else {
+    return E::store(x);
+  }
+}
+
+template <typename E>
+struct Mfma;
+template <>
+struct Mfma<BF16> {
+  using vec8 = bf16x8_t;
+  static __device__ __forceinline__ f32x16_t mma(vec8 a, vec8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<F16> {
+  using vec8 = f16x8_t;
+  static __device__ __forceinline__ f32x16_t mma(vec8 a, vec8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+constexpr int kD = 128;               // head_dim
+constexpr int kKeys = 32;             // keys per tile
+constexpr int kRows = 32;             // query rows per wave (MFMA N)
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * kWave;
+constexpr int kKStride = kD + 8;      // K tile row stride in LDS (elements)
+constexpr int kVStride = kKeys + 4;   // V^T tile row stride in LDS (elements)
+
+template <typename E, int G>
+__global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const AttnArgs a) {
+  using M = Mfma<E>;
+  using vec8 = typename M::vec8;
+  using R = uint16_t;
+  constexpr int BM = kRows * kWaves / G;  // query rows per workgroup
+  using ConstI32 = __attribute__((address_space(4))) const int32_t;
+  __shared__ __attribute__((aligned(16))) R s_k[2][kKeys * kKStride];
+  __shared__ __attribute__((aligned(16))) R s_vt[2][kD * kVStride];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int half = lane / 32;  // which half of the MFMA reduction this lane feeds
+  const int col = lane % 32;   // this lane's query row within the wave's 32
+  const int head = blockIdx.x % a.num_kv_heads;
+  const int qblock = blockIdx.x / a.num_kv_heads;
+  const int g = wave % G;      // query head within the group
+  const int rsub = wave / G;   // 32-row sub-block of the workgroup's rows
+
+  // Request owning this query block (blocks are numbered request by request).
+  const ConstI32* cu_q = (const ConstI32*)(a.cu_q);
+  const ConstI32* cu_k = (const ConstI32*)(a.cu_k);
+  int req = -1, qb0 = 0;
+  for (int r = 0; r < a.num_seqs; ++r) {
+    const int n = (cu_q[r + 1] - cu_q[r] + BM - 1) / BM;
+    if (qblock < qb0 + n) {
+      req = r;
+      break;
+    }
+    qb0 += n;
+  }
+  if (req < 0) return;  // surplus workgroup (uniform)
+  const int q_begin = cu_q[req];
+  const int q_len = cu_q[req + 1] - q_begin;
+  const bool paged = a.tables != nullptr;
+  int ctx = cu_k[req + 1] - cu_k[req];
+  if (paged) ctx = min(ctx, a.t_width * a.block_size);
+  const int64_t krow0 = paged ? 0 : cu_k[req];
+  const int wg_row0 = (qblock - qb0) * BM;
+  const int wg_last = min(q_len, wg_row0 + BM) - 1;
+  // Keys the workgroup needs: up to the causal limit of its last row.
+  int kv_end = max(0, min(ctx, ctx - q_len + wg_last + 1));
+  if (!paged) kv_end = static_cast<int>(min<int64_t>(kv_end, max<int64_t>(a.num_blocks - krow0, 0)));
+  const int ntiles = (kv_end + kKeys - 1) / kKeys;
+
+  const int my_row = wg_row0 + rsub * kRows + col;  // row within the request
+  const bool row_ok = my_row < q_len && rsub * kRows < BM;
+  const int qpos = ctx - q_len + my_row;  // this row sees keys 0 .. qpos
+
+  // Q^T fragments (B operand): k-step ks covers head dims ks*16 .. ks*16+15;
+  // this lane supplies dims ks*16 + half*8 .. +7 of its row.
+  const R* qrow = static_cast<const R*>(a.q) + (q_begin + my_row) * a.q_ts +
+                  (head * G + g) * a.q_hs;
+  vec8 qf[kD / 16];
+#pragma unroll
+  for (int ks = 0; ks < kD / 16; ++ks) {
+    Pack<R, 8> p = zero_pack<R, 8>();
+    if (row_ok) p = load_pack<R, 8>(qrow + ks * 16 + half * 8);
+    qf[ks] = __builtin_bit_cast(vec8, p);
+  }
+
+  // Tile loads: thread t moves chunks t and t + 256 of K and of V (key c / 16,
+  // dims (c % 16) * 8 .. +7), i.e. one key from each 16-key half of the tile.
+  const R* kc = static_cast<const R*>(a.kc);
+  const R* vc = static_cast<const R*>(a.vc);
+  const int32_t* trow = paged ? a.tables + req * a.t_stride : nullptr;
+  const int last_blk = max((kv_end - 1) >> a.log2_block, 0);
+  Pack<R, 8> kreg[2], vreg[2];
+  int blk_ok_mask = 0;  // bit h: the tile's half h has a valid block id
+  auto load_tile = [&](int tile) {
+    const int t0 = tile * kKeys;
+    int ids[2] = {0, 0};
+    bool ok[2] = {true, true};
+    if (paged) {
+      const ConstI32* ctab = (const ConstI32*)(trow);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        ids[h] = ctab[min((t0 + h * 16) >> a.log2_block, last_blk)];
+        ok[h] = ids[h] >= 0 && ids[h] < a.num_blocks;
+      }
+    }
+    blk_ok_mask = (ok[0] ? 1 : 0) | (ok[1] ? 2 : 0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = tid + h * kThreads;
+      const int key = c / 16;
+      const int d0 = (c % 16) * 8;
+      const int pos = t0 + key;
+      const bool valid = pos < kv_end && ok[h];
+      int64_t off;
+      if (paged)
+        off = ids[h] * a.c_bs + (pos & (a.block_size - 1)) * a.c_ts;
+      else
+        off = (krow0 + pos) * a.c_ts;
+      off = valid ? off + head * a.c_hs + d0 : head * a.c_hs + d0;
+      kreg[h] = valid ? load_pack<R, 8>(kc + off) : zero_pack<R, 8>();
+      vreg[h] = valid ? load_pack<R, 8>(vc + off) : zero_pack<R, 8>();
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = tid + h * kThreads;
+      const int key = c / 16;
+      const int d0 = (c % 16) * 8;
+      store_pack<R, 8>(&s_k[buf][key * kKStride + d0], kreg[h]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s_vt[buf][(d0 + j) * kVStride + key] = vreg[h].v[j];
+    }
+  };
+
+  f32x16_t o[kD / 32];
+#pragma unroll
+  for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  const float scale_log2 = a.scale_log2;
+
+  if (ntiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  int mask_cur = blk_ok_mask;
+  __syncthreads();
+  for (int tile = 0; tile < ntiles; ++tile) {
+    const int buf = tile & 1;
+    if (tile + 1 < ntiles) load_tile(tile + 1);
+    const int mask_next = blk_ok_mask;
+
+    // S^T = K . Q^T: s[i] is key (i/4)*8 + half*4 + i%4 of this lane's row.
+    f32x16_t s;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = 0.f;
+    const R* krow = &s_k[buf][col * kKStride + half * 8];
+#pragma unroll
+    for (int ks = 0; ks < kD / 16; ++ks) {
+      const vec8 kf = __builtin_bit_cast(vec8, load_pack<R, 8>(krow + ks * 16));
+      s = M::mma(kf, qf[ks], s);
+    }
+
+    // Scale, mask (causal, past the context, invalid blocks), online softmax.
+    const int t0 = tile * kKeys;
+    float p[16];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = (i / 4) * 8 + half * 4 + (i % 4);
+      const int kpos = t0 + key;
+      const bool ok = row_ok && kpos <= qpos && kpos < kv_end && ((mask_cur >> (key / 16)) & 1);
+      p[i] = ok ? s[i] * scale_log2 : -INFINITY;
+      mt = fmaxf(mt, p[i]);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    const float mnew = fmaxf(m, mt);
+    const float alpha = (mnew == -INFINITY) ? 1.f : fast_exp2(m - mnew);
+    float rs = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      p[i] = (p[i] == -INFINITY) ? 0.f : fast_exp2(p[i] - mnew);
+      rs += p[i];
+    }
+    rs += __shfl_xor(rs, 32, kWave);
+    l = l * alpha + rs;
+    m = mnew;
+#pragma unroll
+    for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+
+    // P^T fragments: reduction slot j of 16-key chunk c is this lane's
+    // p[8c + j], i.e. key 16c + (j/4)*8 + half*4 + j%4.
+    vec8 pf[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      Pack<R, 8> pk;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pk.v[j] = to_raw<E>(p[8 * c + j]);
+      pf[c] = __builtin_bit_cast(vec8, pk);
+    }
+    // O^T += V^T . P^T with the same key mapping on the A side: lane reads
+    // V^T[d][16c + half*4 .. +3] and V^T[d][16c + 8 + half*4 .. +3].
+#pragma unroll
+    for (int db = 0; db < kD / 32; ++db) {
+      const R* vrow = &s_vt[buf][(db * 32 + col) * kVStride + half * 4];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const Pack<R, 4> lo = load_pack<R, 4>(vrow + 16 * c);
+        const Pack<R, 4> hi = load_pack<R, 4>(vrow + 16 * c + 8);
+        Pack<R, 8> vv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          vv.v[j] = lo.v[j];
+          vv.v[4 + j] = hi.v[j];
+        }
+        o[db] = M::mma(__builtin_bit_cast(vec8, vv), pf[c], o[db]);
+      }
+    }
+
+    if (tile + 1 < ntiles) store_tile(buf ^ 1);
+    mask_cur = mask_next;
+    __syncthreads();
+  }
+
+  // o[db][i] = O^T[d = db*32 + (i/4)*8 + half*4 + i%4][row].
+  if (!row_ok) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  R* orow = static_cast<R*>(a.out) + (q_begin + my_row) * a.o_ts + (head * G + g) * a.o_hs;
+#pragma unroll
+  for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      Pack<R, 4> ov;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ov.v[j] = E::store(o[db][qd * 4 + j] * inv);
+      store_pack<R, 4>(orow + db * 32 + qd * 8 + half * 4, ov);
+    }
+}
+
+template <typename E, int G>
+int32_t launch_g(const AttnArgs& a, hipStream_t stream) {
+  constexpr int BM = kRows * kWaves / G;
+  const int64_t blocks = (static_cast<int64_t>(a.num_rows) + BM - 1) / BM + a.num_seqs;
+  const dim3 grid(static_cast<uint32_t>(blocks * a.num_kv_heads));
+  paged_prefill_mfma_kernel<E, G><<<grid, kThreads, 0, stream>>>(a);
+  return check_launch("paged prefill (MFMA)");
+}
+
+template <typename E>
+int32_t launch_typed(const AttnArgs& a, hipStream_t stream) {
+  switch (a.group) {
+    case 1: return launch_g<E, 1>(a, stream);
+    case 2: return launch_g<E, 2>(a, stream);
+    case 4: return launch_g<E, 4>(a, stream);
+    default: return MI_ERR_UNSUPPORTED;
+  }
+}
+
+}  // namespace
+
+bool prefill_mfma_supported(const AttnArgs& a, int32_t dtype) {
+  return (dtype == MI_DTYPE_BF16 || dtype == MI_DTYPE_F16) && a.head_dim == kD &&
+         (a.group == 1 || a.group == 2 || a.group == 4) &&
+         (a.tables == nullptr || a.block_size >= 16);
+}
+
+int32_t launch_prefill_mfma(const AttnArgs& a, int32_t dtype, hipStream_t stream) {
+  if (!prefill_mfma_supported(a, dtype)) return MI_ERR_UNSUPPORTED;
+  return dtype == MI_DTYPE_BF16 ? launch_typed<BF16>(a, stream) : launch_typed<F16>(a, stream);
+}
+
+}  // namespace mi

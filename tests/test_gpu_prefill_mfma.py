@@ -1,0 +1,165 @@
+"""The bf16/f16 MFMA paged-prefill kernel (head_dim 128, GQA groups 1, 2, 4).
+
+Every call here has head_dim 128 and a 16-bit dtype, so mi_paged_prefill
+routes it to the MFMA kernel. Results are compared with the fp32 oracle
+(restating microinfer/layer/paged_attention.py:22-67) at 2e-2 max-abs, the
+decode/prefill tolerance for 16-bit inputs. The cases cover query blocks that
+end inside a 32-row MFMA tile, 32-key tiles that end inside a cache block,
+prefixes shorter and longer than a tile, single-row (decode) requests in the
+same launch, every block size the kernel takes, invalid table entries and
+poison in unused slots, and contiguous K/V.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from microinfer_amd.layer.hip_paged_attention import hip_paged_prefill
+from oracle import dense_causal_attention_f64
+from tests.support import as_f32, max_abs, oracle_prefill
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+D = 128
+
+
+def _paged_case(q_lens, prefixes, hq, hkv, block_size, dtype, seed, poison=False):
+    """Random caches and shuffled block tables for requests with the given
+    query lengths and cached prefixes (context = prefix + query length)."""
+    gen = torch.Generator().manual_seed(seed)
+    contexts = [p + q for p, q in zip(prefixes, q_lens)]
+    nblk = [(c + block_size - 1) // block_size for c in contexts]
+    width = max(nblk)
+    pool = sum(nblk) + 3
+    perm = torch.randperm(pool, generator=gen)
+    tables = torch.full((len(q_lens), width), -1, dtype=torch.int32)
+    used = 0
+    for r, n in enumerate(nblk):
+        tables[r, :n] = perm[used:used + n]
+        used += n
+    fill = 1000.0 if poison else 0.0
+    kc = torch.randn(pool, block_size, hkv, D, generator=gen)
+    vc = torch.randn(pool, block_size, hkv, D, generator=gen)
+    if poison:
+        # Slots past each context hold +-1000: a kernel that reads them fails.
+        for r, c in enumerate(contexts):
+            last = tables[r, nblk[r] - 1]
+            off = c - (nblk[r] - 1) * block_size
+            kc[last, off:] = fill
+            vc[last, off:] = -fill
+        unused = perm[used:]
+        kc[unused] = fill
+        vc[unused] = -fill
+    q = torch.randn(sum(q_lens), hq, D, generator=gen)
+    cu_q = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(contexts)]).astype(np.int32)
+    return (q.to(dtype).to(DEV), kc.to(dtype).to(DEV), vc.to(dtype).to(DEV),
+            tables.to(DEV), contexts, cu_q, cu_k)
+
+
+def _run(q, kc, vc, tables, cu_q, cu_k):
+    return hip_paged_prefill(q, kc, vc, torch.tensor(cu_q, device=DEV),
+                             torch.tensor(cu_k, device=DEV), tables,
+                             max_seqlen_q=int(np.diff(cu_q).max()),
+                             scale=1 / math.sqrt(D))
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_group_sizes_and_tile_edges(hq, hkv, dtype):
+    # Query lengths around the 32-row tile and the workgroup's row block;
+    # prefixes around the 32-key tile and the 16-token block.
+    q_lens = [1, 31, 32, 33, 70, 129]
+    prefixes = [0, 1, 15, 16, 47, 300]
+    q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, hq, hkv, 16, dtype, 1)
+    out = _run(q, kc, vc, tables, cu_q, cu_k)
+    expected = oracle_prefill(q, kc, vc, tables, contexts, cu_q, 1 / math.sqrt(D))
+    assert max_abs(out, expected) <= 2e-2
+
+
+@pytest.mark.parametrize("block_size", [16, 32, 64, 128, 256])
+def test_block_sizes(block_size):
+    q_lens = [5, 64, 100]
+    prefixes = [block_size - 3, 2 * block_size + 1, 0]
+    q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, 32, 8, block_size,
+                                                          torch.bfloat16, 2)
+    out = _run(q, kc, vc, tables, cu_q, cu_k)
+    expected = oracle_prefill(q, kc, vc, tables, contexts, cu_q, 1 / math.sqrt(D))
+    assert max_abs(out, expected) <= 2e-2
+
+
+def test_poison_in_unused_slots_is_never_read():
+    q_lens = [17, 64, 1]
+    prefixes = [10, 100, 250]
+    q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, 16, 8, 16,
+                                                          torch.bfloat16, 3, poison=True)
+    out = _run(q, kc, vc, tables, cu_q, cu_k)
+    assert torch.isfinite(out).all()
+    expected = oracle_prefill(q, kc, vc, tables, contexts, cu_q, 1 / math.sqrt(D))
+    assert max_abs(out, expected) <= 2e-2
+
+
+def test_invalid_table_entries_are_masked():
+    # A -1 and an out-of-range id inside the contexts: those blocks drop out
+    # of the softmax (as in the decode kernel) and are never dereferenced.
+    q_lens = [40, 20]
+    prefixes = [60, 10]
+    q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, 16, 8, 16,
+                                                          torch.bfloat16, 4)
+    bad = tables.clone()
+    bad[0, 1] = -1
+    bad[1, 0] = 10 ** 6
+    out = _run(q, kc, vc, bad, cu_q, cu_k)
+    assert torch.isfinite(out).all()
+    # Expected: the same attention with those blocks' keys excluded.
+    host_t = bad.cpu().numpy()
+    ref = np.zeros(as_f32(out).shape, dtype=np.float64)
+    kf, vf, qf = as_f32(kc), as_f32(vc), as_f32(q)
+    for r in range(2):
+        c, ql = contexts[r], q_lens[r]
+        pos = np.arange(c)
+        blk = host_t[r, pos // 16]
+        keep = (blk >= 0) & (blk < kc.shape[0])
+        ks = np.where(keep[:, None, None], kf[np.clip(blk, 0, kc.shape[0] - 1), pos % 16], 0)
+        vs = np.where(keep[:, None, None], vf[np.clip(blk, 0, kc.shape[0] - 1), pos % 16], 0)
+        for i in range(ql):
+            row = cu_q[r] + i
+            visible = keep & (pos <= c - ql + i)
+            for h in range(16):
+                s = (ks[:, h // 2] @ qf[row, h]) / math.sqrt(D)
+                s = np.where(visible, s, -np.inf)
+                if not visible.any():
+                    continue
+                w = np.exp(s - s.max())
+                ref[row, h] = (w / w.sum()) @ vs[:, h // 2]
+    assert np.abs(as_f32(out) - ref).max() <= 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_contiguous_kv_matches_dense(dtype):
+    torch.manual_seed(5)
+    q_lens = [33, 1, 128, 7]
+    total = sum(q_lens)
+    q = torch.randn(total, 16, D, device=DEV).to(dtype)
+    k = torch.randn(total, 8, D, device=DEV).to(dtype)
+    v = torch.randn(total, 8, D, device=DEV).to(dtype)
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    cu_t = torch.tensor(cu, device=DEV)
+    out = hip_paged_prefill(q, k, v, cu_t, cu_t, None, max_seqlen_q=max(q_lens))
+    expected = np.concatenate([
+        dense_causal_attention_f64(as_f32(q[a:b]), as_f32(k[a:b]), as_f32(v[a:b]),
+                                   scale=1 / math.sqrt(D))
+        for a, b in zip(cu[:-1], cu[1:])
+    ])
+    assert max_abs(out, expected) <= 2e-2
+
+
+def test_long_prefix_chunk():
+    # One 512-row chunk on a 3000-token prefix (the cfg4 shape of one request).
+    q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case([512], [3000], 32, 8, 16,
+                                                          torch.bfloat16, 6)
+    out = _run(q, kc, vc, tables, cu_q, cu_k)
+    expected = oracle_prefill(q, kc, vc, tables, contexts, cu_q, 1 / math.sqrt(D))
+    assert max_abs(out, expected) <= 2e-2
