@@ -221,16 +221,20 @@ def run_prefill(args) -> int:
 
     step()
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
+    if args.no_graph:
+        run = step
+    else:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        run = graph.replay
     for _ in range(args.warmup):
-        graph.replay()
+        run()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(args.steps):
-        graph.replay()
+        run()
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps

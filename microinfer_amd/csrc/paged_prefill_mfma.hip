@@ -103,7 +103,9 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
   int ctx = cu_k[req + 1] - cu_k[req];
   if (paged) ctx = min(ctx, a.t_width * a.block_size);
   const int64_t krow0 = paged ? 0 : cu_k[req];
-  const int wg_row0 = (qblock - qb0) * BM;
+  // Within a request the last query block (the most keys) runs first.
+  const int nblocks_req = (q_len + BM - 1) / BM;
+  const int wg_row0 = (nblocks_req - 1 - (qblock - qb0)) * BM;
   const int wg_last = min(q_len, wg_row0 + BM) - 1;
   // Keys the workgroup needs: up to the causal limit of its last row.
   int kv_end = max(0, min(ctx, ctx - q_len + wg_last + 1));
@@ -113,6 +115,8 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
   const int my_row = wg_row0 + rsub * kRows + col;  // row within the request
   const bool row_ok = my_row < q_len && rsub * kRows < BM;
   const int qpos = ctx - q_len + my_row;  // this row sees keys 0 .. qpos
+  // Causal limit of the wave's first row (the smallest of the wave's rows).
+  const int qpos_first = ctx - q_len + wg_row0 + rsub * kRows;
 
   // Q^T fragments (B operand): k-step ks covers head dims ks*16 .. ks*16+15;
   // this lane supplies dims ks*16 + half*8 .. +7 of its row.
@@ -132,9 +136,13 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
   const R* vc = static_cast<const R*>(a.vc);
   const int32_t* trow = paged ? a.tables + req * a.t_stride : nullptr;
   const int last_blk = max((kv_end - 1) >> a.log2_block, 0);
-  Pack<R, 8> kreg[2], vreg[2];
-  int blk_ok_mask = 0;  // bit h: the tile's half h has a valid block id
-  auto load_tile = [&](int tile) {
+  // Two register sets: the loads of tile t are issued two tiles ahead (at
+  // the start of tile t - 2) and written to LDS at the end of tile t - 1.
+  struct Stage {
+    Pack<R, 8> k[2], v[2];
+    int mask;  // bit h: the tile's 16-key half h has a valid block id
+  };
+  auto load_tile = [&](int tile, Stage& st) {
     const int t0 = tile * kKeys;
     int ids[2] = {0, 0};
     bool ok[2] = {true, true};
@@ -146,33 +154,40 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
         ok[h] = ids[h] >= 0 && ids[h] < a.num_blocks;
       }
     }
-    blk_ok_mask = (ok[0] ? 1 : 0) | (ok[1] ? 2 : 0);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int c = tid + h * kThreads;
-      const int key = c / 16;
-      const int d0 = (c % 16) * 8;
+    st.mask = (ok[0] ? 1 : 0) | (ok[1] ? 2 : 0);
+    // Row offset of tile key `key`, or the head's first row (always in
+    // bounds; its scores are masked) when the key is past the range or in a
+    // block with an invalid id.
+    auto row_off = [&](int key) {
       const int pos = t0 + key;
-      const bool valid = pos < kv_end && ok[h];
+      const int hh = key / 16;
+      const bool valid = pos < kv_end && ok[hh];
       int64_t off;
       if (paged)
-        off = ids[h] * a.c_bs + (pos & (a.block_size - 1)) * a.c_ts;
+        off = ids[hh] * a.c_bs + (pos & (a.block_size - 1)) * a.c_ts;
       else
         off = (krow0 + pos) * a.c_ts;
-      off = valid ? off + head * a.c_hs + d0 : head * a.c_hs + d0;
-      kreg[h] = valid ? load_pack<R, 8>(kc + off) : zero_pack<R, 8>();
-      vreg[h] = valid ? load_pack<R, 8>(vc + off) : zero_pack<R, 8>();
+      return valid ? off + head * a.c_hs : head * a.c_hs;
+    };
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      // K: 16 consecutive threads read one key's 256-byte row (coalesced).
+      const int c = tid + h * kThreads;
+      st.k[h] = load_pack<R, 8>(kc + row_off(c / 16) + (c % 16) * 8);
+      // V: a wave's lanes take 32 keys x 2 column chunks, so its transposed
+      // LDS stores (lane = key) fall in distinct banks.
+      st.v[h] = load_pack<R, 8>(vc + row_off(c % 32) + (c / 32) * 8);
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](int buf, const Stage& st) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int c = tid + h * kThreads;
-      const int key = c / 16;
-      const int d0 = (c % 16) * 8;
-      store_pack<R, 8>(&s_k[buf][key * kKStride + d0], kreg[h]);
+      store_pack<R, 8>(&s_k[buf][(c / 16) * kKStride + (c % 16) * 8], st.k[h]);
+      const int key = c % 32;
+      const int d0 = (c / 32) * 8;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) s_vt[buf][(d0 + j) * kVStride + key] = vreg[h].v[j];
+      for (int j = 0; j < 8; ++j) s_vt[buf][(d0 + j) * kVStride + key] = st.v[h].v[j];
     }
   };
 
@@ -184,56 +199,73 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
   float m = -INFINITY, l = 0.f;
   const float scale_log2 = a.scale_log2;
 
-  if (ntiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  int mask_cur = blk_ok_mask;
-  __syncthreads();
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int buf = tile & 1;
-    if (tile + 1 < ntiles) load_tile(tile + 1);
-    const int mask_next = blk_ok_mask;
-
+  // One 32-key tile from LDS buffer `buf`.
+  auto compute = [&](int tile, int buf, int mask) {
     // S^T = K . Q^T: s[i] is key (i/4)*8 + half*4 + i%4 of this lane's row.
-    f32x16_t s;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = 0.f;
-    const R* krow = &s_k[buf][col * kKStride + half * 8];
-#pragma unroll
-    for (int ks = 0; ks < kD / 16; ++ks) {
-      const vec8 kf = __builtin_bit_cast(vec8, load_pack<R, 8>(krow + ks * 16));
-      s = M::mma(kf, qf[ks], s);
-    }
-
-    // Scale, mask (causal, past the context, invalid blocks), online softmax.
-    const int t0 = tile * kKeys;
-    float p[16];
-    float mt = -INFINITY;
+    // Two independent accumulation chains (head dims 0-63 and 64-127) keep
+    // the MFMA pipeline fed; they are summed once.
+    f32x16_t s, s2;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int key = (i / 4) * 8 + half * 4 + (i % 4);
-      const int kpos = t0 + key;
-      const bool ok = row_ok && kpos <= qpos && kpos < kv_end && ((mask_cur >> (key / 16)) & 1);
-      p[i] = ok ? s[i] * scale_log2 : -INFINITY;
-      mt = fmaxf(mt, p[i]);
+      s[i] = 0.f;
+      s2[i] = 0.f;
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-    const float mnew = fmaxf(m, mt);
-    const float alpha = (mnew == -INFINITY) ? 1.f : fast_exp2(m - mnew);
+    const R* krow = &s_k[buf][col * kKStride + half * 8];
+#pragma unroll
+    for (int ks = 0; ks < kD / 32; ++ks) {
+      const vec8 k0 = __builtin_bit_cast(vec8, load_pack<R, 8>(krow + ks * 16));
+      const vec8 k1 = __builtin_bit_cast(vec8, load_pack<R, 8>(krow + (ks + kD / 32) * 16));
+      s = M::mma(k0, qf[ks], s);
+      s2 = M::mma(k1, qf[ks + kD / 32], s2);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] += s2[i];
+
+    // Mask (causal, past the workgroup's keys, invalid blocks) only where the
+    // tile reaches one of those limits for some row of the wave; interior
+    // tiles skip it. Rows past the request are left unmasked: their lanes'
+    // states are never stored.
+    const int t0 = tile * kKeys;
+    const bool interior = t0 + kKeys <= kv_end && mask == 3 && t0 + kKeys - 1 <= qpos_first;
+    float smax = -INFINITY;
+    if (interior) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) smax = fmaxf(smax, s[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = (i / 4) * 8 + half * 4 + (i % 4);
+        const int kpos = t0 + key;
+        const bool ok = kpos <= qpos && kpos < kv_end && ((mask >> (key / 16)) & 1);
+        s[i] = ok ? s[i] : -INFINITY;
+        smax = fmaxf(smax, s[i]);
+      }
+    }
+    // Online softmax in the log2 domain on scaled scores s * c (c > 0, so the
+    // maximum can be taken on raw scores). The running maximum m is moved --
+    // and O and l rescaled -- only when some row's tile maximum exceeds it by
+    // more than 8, a wave-uniform decision; otherwise exponents stay below
+    // 2^8 and the normalisation by l at the end is unchanged.
+    smax = fmaxf(smax, __shfl_xor(smax, 32, kWave)) * scale_log2;
+    if (__ballot(smax > m + 8.f) != 0) {
+      const float mnew = fmaxf(m, smax);
+      const float alpha = (mnew == -INFINITY) ? 1.f : fast_exp2(m - mnew);
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+      m = mnew;
+    }
+    const float neg_m = m == -INFINITY ? 0.f : -m;  // all scores masked so far: p = 0
+    float p[16];
     float rs = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      p[i] = (p[i] == -INFINITY) ? 0.f : fast_exp2(p[i] - mnew);
+      p[i] = fast_exp2(fmaf(s[i], scale_log2, neg_m));
       rs += p[i];
     }
-    rs += __shfl_xor(rs, 32, kWave);
-    l = l * alpha + rs;
-    m = mnew;
-#pragma unroll
-    for (int db = 0; db < kD / 32; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+    l += rs + __shfl_xor(rs, 32, kWave);
 
     // P^T fragments: reduction slot j of 16-key chunk c is this lane's
     // p[8c + j], i.e. key 16c + (j/4)*8 + half*4 + j%4.
@@ -263,9 +295,37 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
         o[db] = M::mma(__builtin_bit_cast(vec8, vv), pf[c], o[db]);
       }
     }
+  };
 
-    if (tile + 1 < ntiles) store_tile(buf ^ 1);
-    mask_cur = mask_next;
+  // Pipeline, unrolled by two so each register set and LDS buffer has a
+  // fixed role: step t computes tile t from buffer t % 2, issues the loads of
+  // tile t + 2 into set t % 2 and stores set (t + 1) % 2 (tile t + 1) into
+  // buffer (t + 1) % 2. Loads past the last tile re-read the last tile and
+  // are never stored.
+  Stage st0, st1;
+  int mb0 = 0, mb1 = 0;  // masks of the tiles held in LDS buffers 0 and 1
+  if (ntiles > 0) {
+    load_tile(0, st0);
+    load_tile(min(1, ntiles - 1), st1);
+    store_tile(0, st0);
+    mb0 = st0.mask;
+  }
+  __syncthreads();
+  for (int t = 0; t < ntiles; t += 2) {
+    load_tile(min(t + 2, ntiles - 1), st0);
+    compute(t, 0, mb0);
+    if (t + 1 < ntiles) {
+      store_tile(1, st1);
+      mb1 = st1.mask;
+    }
+    __syncthreads();
+    if (t + 1 >= ntiles) break;
+    load_tile(min(t + 3, ntiles - 1), st1);
+    compute(t + 1, 1, mb1);
+    if (t + 2 < ntiles) {
+      store_tile(0, st0);
+      mb0 = st0.mask;
+    }
     __syncthreads();
   }
 
