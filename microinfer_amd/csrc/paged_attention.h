@@ -39,6 +39,7 @@ struct AttnArgs {
   int64_t nk_ts, nk_hs, nv_ts, nv_hs;
   int32_t num_seqs;  // decode: sequences; varlen: requests
   int32_t num_rows;  // varlen: query rows
+  int32_t max_q;     // varlen: no request has more query rows (launch shape)
   int32_t num_kv_heads, group, head_dim, block_size, log2_block, num_blocks;
   int32_t split_k;          // 0 = adaptive partitions
   int32_t target_items;     // adaptive: aim for about this many (item, head) groups

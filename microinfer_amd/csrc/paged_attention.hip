@@ -259,6 +259,8 @@ extern "C" int32_t mi_paged_prefill(
   if (num_tokens == 0) return MI_OK;
   if (num_requests == 0)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_prefill: tokens without requests");
+  if (max_seqlen_q == 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_prefill: max_seqlen_q must be positive");
   // block_tables may be NULL: contiguous varlen K/V (see mi_attn.h).
   if (!query || !key_cache || !value_cache || !cu_seqlens_q || !cu_seqlens_k || !out)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_prefill: null pointer");
@@ -290,6 +292,7 @@ extern "C" int32_t mi_paged_prefill(
   a.o_hs = out_head_stride;
   a.num_seqs = num_requests;
   a.num_rows = num_tokens;
+  a.max_q = max_seqlen_q;
   a.num_kv_heads = num_kv_heads;
   a.group = num_q_heads / num_kv_heads;
   a.head_dim = head_dim;

@@ -39,6 +39,16 @@ __device__ __forceinline__ uint16_t to_raw(float x) {
   }
 }
 
+// The value held by lane ^ 32 (the other half of a query row's keys), with
+// v_permlane32_swap (a VALU op; no LDS round trip). The instruction swaps the
+// upper half of its first operand with the lower half of its second: lanes
+// 0-31 find their partner in the second result, lanes 32-63 in the first.
+__device__ __forceinline__ float partner32(float v, int lane) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, lane < 32 ? r[1] : r[0]);
+}
+
 template <typename E>
 struct Mfma;
 template <>
@@ -59,10 +69,14 @@ struct Mfma<F16> {
 constexpr int kD = 128;               // head_dim
 constexpr int kKeys = 32;             // keys per tile
 constexpr int kRows = 32;             // query rows per wave (MFMA N)
-constexpr int kWaves = 4;
+#ifndef MI_PREFILL_WAVES
+#define MI_PREFILL_WAVES 4
+#endif
+constexpr int kWaves = MI_PREFILL_WAVES;  // waves per workgroup
 constexpr int kThreads = kWaves * kWave;
 constexpr int kKStride = kD + 8;      // K tile row stride in LDS (elements)
 constexpr int kVStride = kKeys + 4;   // V^T tile row stride in LDS (elements)
+constexpr int kPerThread = kKeys * kD / 8 / kThreads;  // 16-byte chunks per thread
 
 template <typename E, int G>
 __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const AttnArgs a) {
@@ -84,7 +98,8 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
   const int g = wave % G;      // query head within the group
   const int rsub = wave / G;   // 32-row sub-block of the workgroup's rows
 
-  // Request owning this query block (blocks are numbered request by request).
+  // Request owning this query block (blocks are numbered request by request,
+  // so the blocks of one request -- which share its K/V in L2 -- run together).
   const ConstI32* cu_q = (const ConstI32*)(a.cu_q);
   const ConstI32* cu_k = (const ConstI32*)(a.cu_k);
   int req = -1, qb0 = 0;
@@ -139,7 +154,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
   // Two register sets: the loads of tile t are issued two tiles ahead (at
   // the start of tile t - 2) and written to LDS at the end of tile t - 1.
   struct Stage {
-    Pack<R, 8> k[2], v[2];
+    Pack<R, 8> k[kPerThread], v[kPerThread];
     int mask;  // bit h: the tile's 16-key half h has a valid block id
   };
   auto load_tile = [&](int tile, Stage& st) {
@@ -170,7 +185,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
       return valid ? off + head * a.c_hs : head * a.c_hs;
     };
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < kPerThread; ++h) {
       // K: 16 consecutive threads read one key's 256-byte row (coalesced).
       const int c = tid + h * kThreads;
       st.k[h] = load_pack<R, 8>(kc + row_off(c / 16) + (c % 16) * 8);
@@ -181,7 +196,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
   };
   auto store_tile = [&](int buf, const Stage& st) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < kPerThread; ++h) {
       const int c = tid + h * kThreads;
       store_pack<R, 8>(&s_k[buf][(c / 16) * kKStride + (c % 16) * 8], st.k[h]);
       const int key = c % 32;
@@ -246,7 +261,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
     // and O and l rescaled -- only when some row's tile maximum exceeds it by
     // more than 8, a wave-uniform decision; otherwise exponents stay below
     // 2^8 and the normalisation by l at the end is unchanged.
-    smax = fmaxf(smax, __shfl_xor(smax, 32, kWave)) * scale_log2;
+    smax = fmaxf(smax, partner32(smax, lane)) * scale_log2;
     if (__ballot(smax > m + 8.f) != 0) {
       const float mnew = fmaxf(m, smax);
       const float alpha = (mnew == -INFINITY) ? 1.f : fast_exp2(m - mnew);
@@ -265,7 +280,10 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
       p[i] = fast_exp2(fmaf(s[i], scale_log2, neg_m));
       rs += p[i];
     }
-    l += rs + __shfl_xor(rs, 32, kWave);
+    // Same sum on both halves: lower half adds (own, partner), upper half
+    // (partner, own), i.e. always (lane l & 31) + (lane l | 32).
+    const float other = partner32(rs, lane);
+    l += lane < 32 ? rs + other : other + rs;
 
     // P^T fragments: reduction slot j of 16-key chunk c is this lane's
     // p[8c + j], i.e. key 16c + (j/4)*8 + half*4 + j%4.
