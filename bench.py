@@ -87,6 +87,20 @@ def build_decode_state(torch, layers: int, layout: str):
     )
 
 
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "paged_decode_traffic_qwen3-0.6b_b32.json")
+
+
+def measured_traffic():
+    """HBM bytes per decode launch from the committed FETCH_SIZE / WRITE_SIZE runs
+    (calibrated against a copy kernel), or None when that profile is absent."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            return int(json.load(f)["traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def copy_calibration(torch, mib: int) -> None:
     """One plain device-to-device copy of ``mib`` MiB (reads and writes that many)."""
     src = torch.empty(mib << 20, dtype=torch.uint8, device="cuda")
@@ -403,7 +417,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "kernel": "paged_attention_vector_kernel (fused append + decode + split merge)",
             "bytes_per_launch": layer_bytes,
             "us_per_launch": round(layer_us, 3),
