@@ -272,8 +272,8 @@ def run_prefill(args) -> int:
             "workload": ("mixed chunked prefill, Qwen3-8B attention (32 Q / 8 KV heads, "
                          "head_dim 128), bf16, block 16, pool 65536 blocks: 8 chunks of 512 "
                          "rows on prefixes U[0,3072] (first 1024 tokens shared) + 24 decode "
-                         "rows with contexts U[256,2048] (seed 0), one varlen launch, hipGraph "
-                         "replay"),
+                         "rows with contexts U[256,2048] (seed 0), one varlen launch per step, "
+                         + ("launched eagerly" if args.no_graph else "hipGraph replay")),
             "query_rows": total_q,
             "flops_per_launch": flops,
             "kv_layout": args.layout,
@@ -297,6 +297,183 @@ def run_prefill(args) -> int:
     return 0
 
 
+class _DecodeSeq:
+    """The attributes of a scheduled sequence that the metadata build reads."""
+
+    __slots__ = ("token_ids", "last_token", "block_table", "num_cached_tokens",
+                 "num_scheduled_tokens")
+
+    def __init__(self, token_ids, block_table):
+        self.token_ids = token_ids
+        self.last_token = token_ids[-1]
+        self.block_table = block_table
+        self.num_cached_tokens = len(token_ids) - 1
+        self.num_scheduled_tokens = 1
+
+    def __len__(self):
+        return len(self.token_ids)
+
+    def __getitem__(self, key):
+        return self.token_ids[key]
+
+
+def run_step_metadata(args) -> int:
+    """Decode-step metadata of the 0.6B engine shape: 64 running requests
+    (128-token prompts, up to 16 generated tokens), pool 4096 blocks + the pad
+    block, block 16, written into the 64-row graph bucket at table width 4097."""
+    import torch
+
+    from microinfer_amd import _lib
+    from microinfer_amd.runner import StepMetadataBuilder
+
+    dev = torch.device("cuda", 0)
+    num_blocks, block_size, batch, prompt, gen_tokens = 4096, 16, 64, 128, 16
+    width = num_blocks + 1
+    rng = np.random.default_rng(0)
+    perm = rng.permutation(num_blocks).tolist()
+    steps = []  # one list of sequences per decode step, built before timing
+    for t in range(gen_tokens):
+        seqs = []
+        for r in range(batch):
+            length = prompt + 1 + t
+            blocks = perm[r * 10:r * 10 + (length + block_size - 1) // block_size]
+            seqs.append(_DecodeSeq(rng.integers(0, 151936, length).tolist(), blocks))
+        steps.append(seqs)
+    builder = StepMetadataBuilder(block_size, dev, pad_block_id=num_blocks)
+    buffers = builder.pad_buffers(batch, width)
+
+    def run(k, sync):
+        for i in range(k):
+            builder.fill_decode(buffers, steps[i % gen_tokens], rows=batch)
+            if sync:  # an engine reads the step's tokens back before the next step
+                torch.cuda.synchronize()
+
+    run(args.warmup, True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run(args.steps, True)
+    us_per_step = (time.perf_counter() - t0) / args.steps * 1e6
+    t0 = time.perf_counter()
+    run(args.steps, False)
+    host_us = (time.perf_counter() - t0) / args.steps * 1e6
+    torch.cuda.synchronize()
+    log(f"{us_per_step:.1f} us per synchronised step, {host_us:.1f} us host per pipelined step")
+
+    # Kernel alone, timed with events on the stream it is launched on (the
+    # compact description of the last step is still in the builder's upload).
+    lib = _lib.load()
+    seqs = steps[-1]
+    lengths = np.array([len(s) for s in seqs], dtype=np.int32)
+    counts = np.array([len(s.block_table) for s in seqs], dtype=np.int32)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    blocks = np.concatenate([s.block_table for s in seqs]).astype(np.int32)
+    compact = torch.tensor(np.concatenate([np.arange(batch + 1, dtype=np.int32), lengths - 1,
+                                           offsets, blocks]), device=dev)
+    tokens = torch.tensor([s.last_token for s in seqs], dtype=torch.int64, device=dev)
+    cu_q, starts = compact[:batch + 1], compact[batch + 1:2 * batch + 1]
+    d_offsets, d_blocks = compact[2 * batch + 1:3 * batch + 2], compact[3 * batch + 2:]
+    stream = _lib.stream_handle(dev)
+
+    def launch():
+        _lib.check(lib.mi_step_metadata(
+            cu_q.data_ptr(), starts.data_ptr(), d_offsets.data_ptr(), d_blocks.data_ptr(),
+            tokens.data_ptr(), batch, batch, batch, block_size, num_blocks,
+            buffers.block_tables.data_ptr(), width, width, buffers.context_lens.data_ptr(),
+            buffers.slot_mapping.data_ptr(), buffers.positions.data_ptr(),
+            buffers.input_ids.data_ptr(), stream), "mi_step_metadata")
+
+    for _ in range(args.warmup):
+        launch()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        launch()
+    end.record()
+    torch.cuda.synchronize()
+    kernel_us = start.elapsed_time(end) / args.steps * 1e3
+    # Algorithmic bytes: the table and four per-row outputs written, the
+    # compact description read.
+    nbytes = batch * width * 4 + batch * (8 + 8 + 4 + 4) + compact.numel() * 4 + batch * 8
+    achieved = nbytes / (kernel_us * 1e-6) / 1e9
+    result = {
+        "metric": "decode step metadata build us/step (64-row graph bucket, table width 4097)",
+        "value": round(us_per_step, 2),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_per_step / 1e3, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32",
+        "data": "synthetic: 64 decode sequences, random token ids and disjoint block tables",
+        "config": {
+            "workload": ("decode-step metadata for the Qwen3-0.6B engine run: 64 requests, "
+                         "contexts 129-144, block 16, pool 4096 + 1 pad block, bucket 64 at "
+                         "width 4097; host packing + one pinned upload + one expansion launch "
+                         "per step"),
+            "host_us_per_step_pipelined": round(host_us, 2),
+            "timing": "each timed step ends with a device synchronisation, as an engine "
+                      "step does when it reads its sampled tokens",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "step_metadata_kernel",
+            "bytes_per_launch": nbytes,
+            "us_per_launch": round(kernel_us, 3),
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = step_metadata_cpu_baseline(torch, steps, builder, batch,
+                                                           width, num_blocks, dev)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def step_metadata_cpu_baseline(torch, steps, builder, batch, width, num_blocks, dev,
+                               samples: int = 200):
+    """The reference's host build: every row filled on the CPU (the oracle's
+    restatement of runner.py:160-176, :561-576) and the five arrays, the
+    table at full width, copied to the device from pinned memory."""
+    from oracle.step_metadata import decode_rows
+
+    pinned = {}
+    device = {}
+
+    def one(seqs):
+        rows = decode_rows(seqs, builder.block_size, rows=batch, width=width,
+                           pad_block=num_blocks)
+        for key, array in rows.items():
+            if key not in pinned:
+                pinned[key] = torch.empty(array.shape, dtype=torch.from_numpy(array).dtype,
+                                          pin_memory=True)
+                device[key] = torch.empty_like(pinned[key], device=dev)
+            pinned[key].numpy()[...] = array
+            device[key].copy_(pinned[key], non_blocking=True)
+        torch.cuda.synchronize()
+
+    one(steps[0])
+    t0 = time.perf_counter()
+    for i in range(samples):
+        one(steps[i % len(steps)])
+    per = (time.perf_counter() - t0) / samples
+    return {
+        "value": round(per * 1e6, 2),
+        "unit": "us/step",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{samples} decode steps of the same workload: rows filled on the host by "
+                   "the oracle's restatement of the runner, then 5 pinned copies "
+                   f"including the full-width table, synchronised each step ({cpu_model()})"),
+    }
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -305,9 +482,11 @@ def main() -> int:
     parser.add_argument("--layers", type=int, default=28)
     parser.add_argument("--layout", default="head_major", choices=["head_major", "token_major"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--workload", default="decode", choices=["decode", "prefill"],
+    parser.add_argument("--workload", default="decode",
+                        choices=["decode", "prefill", "step-metadata"],
                         help="decode: the headline paged-decode line; prefill: the mixed "
-                             "chunked-prefill (MFMA) line")
+                             "chunked-prefill (MFMA) line; step-metadata: the decode step's "
+                             "device-built metadata")
     parser.add_argument("--no-graph", action="store_true",
                         help="launch the step eagerly (for per-dispatch counter runs)")
     parser.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -323,6 +502,8 @@ def main() -> int:
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     if args.workload == "prefill":
         return run_prefill(args)
+    if args.workload == "step-metadata":
+        return run_step_metadata(args)
 
     import torch
 
@@ -404,7 +585,7 @@ def main() -> int:
             "workload": ("paged decode + KV append, Qwen3-0.6B attention (16 Q / 8 KV heads, "
                          "head_dim 128), bf16, block 16, pool 16384 blocks per layer, "
                          "32 sequences, contexts U[128,2048] (seed 0), 28 independent layer "
-                         "caches, hipGraph replay"),
+                         "caches, " + ("launched eagerly" if args.no_graph else "hipGraph replay")),
             "layers": args.layers,
             "sum_context_tokens": int(np.sum(contexts)),
             "kv_layout": args.layout,

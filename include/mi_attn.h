@@ -241,6 +241,44 @@ int32_t mi_gather_kv(const void* key_cache, const void* value_cache,
                      int32_t head_dim, int32_t block_size, int32_t num_blocks,
                      int32_t dtype, void* stream);
 
+/*
+ * Per-step index metadata, expanded on the device from a compact description
+ * of the scheduled batch (all pointers device memory, int32 unless noted).
+ *
+ * Row r < num_seqs schedules q_r = cu_seqlens_q[r+1] - cu_seqlens_q[r] tokens
+ * at positions starts[r] .. starts[r] + q_r - 1 and owns the block ids
+ * blocks[block_offsets[r] .. block_offsets[r+1]) (n_r of them). Written:
+ *   context_lens[r]       = starts[r] + q_r
+ *   block_tables[r][c]    = c < n_r ? blocks[block_offsets[r] + c] : -1, c < width
+ *   for t = cu_seqlens_q[r] + i:
+ *     positions[t] (int64) = p = starts[r] + i
+ *     slot_mapping[t]      = table[p / block_size] * block_size + p % block_size
+ *                            (-1 when p / block_size >= n_r)
+ *     input_ids[t] (int64) = token_ids[t]
+ * Rows num_seqs .. rows-1 are graph pad rows, one token each at
+ * t = cu_seqlens_q[num_seqs] + (r - num_seqs): input id 0, position 0,
+ * context 1, slot pad_block * block_size + r % block_size, table
+ * [pad_block, -1, ...].
+ *
+ * Replaces ModelRunner._fill_decode_rows + _copy_decode_buffers
+ * (microinfer/runner.py:160-188), the pad rows of _fill_pad_buffers /
+ * _fill_graph_bucket (:203-215, :561-576), prepare_decode (:348-385) and the
+ * token lists of prepare_prefill (:298-346). Decode is the case q_r = 1,
+ * starts[r] = len - 1. Any output pointer may be NULL (not written).
+ * num_tokens = cu_seqlens_q[num_seqs] + rows - num_seqs bounds every token
+ * store; block_offsets must be nondecreasing with blocks holding
+ * block_offsets[num_seqs] ids, and token_ids cu_seqlens_q[num_seqs] ids.
+ * Capture-safe (one launch, no allocation).
+ */
+int32_t mi_step_metadata(const int32_t* cu_seqlens_q, const int32_t* starts,
+                         const int32_t* block_offsets, const int32_t* blocks,
+                         const int64_t* token_ids, int32_t num_seqs, int32_t rows,
+                         int32_t num_tokens, int32_t block_size, int32_t pad_block,
+                         int32_t* block_tables, int64_t block_table_stride,
+                         int32_t block_table_width, int32_t* context_lens,
+                         int32_t* slot_mapping, int64_t* positions, int64_t* input_ids,
+                         void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

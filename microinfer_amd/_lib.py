@@ -59,6 +59,11 @@ SIGNATURES = {
         [_P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P, _I32, _I32, _P, _P, _I32, _I32,
          _I32, _I32, _I32, _P],
     ),
+    "mi_step_metadata": (
+        _I32,
+        [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _I64, _I32, _P, _P, _P, _P,
+         _P],
+    ),
 }
 
 _lock = threading.Lock()

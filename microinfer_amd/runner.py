@@ -1,0 +1,389 @@
+"""Per-step attention metadata built on the device, and graph-captured decode.
+
+Mirrors the metadata half of ``ModelRunner`` (microinfer/runner.py):
+``prepare_prefill`` (:298-346), ``prepare_decode`` (:348-385),
+``prepare_block_tables`` (:290-296), the decode buffers of ``_DecodeBuffers``
+(:16-48), the graph buckets of ``capture_cuda_graphs`` (:275-283), the pad
+rows of ``_fill_pad_buffers`` / ``_fill_graph_bucket`` (:203-215, :561-576)
+and the bucket capture and replay of ``_capture_bucket`` / ``_run_decode``
+(:217-250, :578-604).
+
+The reference fills every row in Python and copies full-width tables to the
+device each step (``[bucket, num_blocks + 1]`` int32 for a graph bucket).
+Here the host packs only what the scheduler decided -- each sequence's first
+scheduled position, its token count, the block ids it owns and the scheduled
+token ids -- into a pinned buffer, sends it with one asynchronous copy, and
+``mi_step_metadata`` expands it on the device into the int32/int64 tensors the
+attention kernels and the model read.
+
+A scheduled sequence is any object with ``len()``, slicing over its token ids,
+``last_token``, ``block_table``, ``num_cached_tokens`` and
+``num_scheduled_tokens`` (``microinfer/engine/sequence.py:14-45``).
+"""
+
+from __future__ import annotations
+
+from itertools import chain
+
+import numpy as np
+import torch
+
+from microinfer_amd import _lib
+from microinfer_amd.layer.metadata import AttentionMetadata
+
+_INT32_MAX = 2 ** 31 - 1
+
+
+def graph_buckets(max_num_seqs: int) -> list[int]:
+    """Decode batch sizes captured as graphs: 1, 2, 4, 8, multiples of 16 and
+    ``max_num_seqs`` itself (microinfer/runner.py:275-283)."""
+    if max_num_seqs < 1:
+        raise ValueError("max_num_seqs must be positive")
+    buckets = sorted({b for b in [1, 2, 4, 8, *range(16, max_num_seqs + 1, 16)]
+                      if b <= max_num_seqs})
+    if buckets[-1] != max_num_seqs:
+        buckets.append(max_num_seqs)
+    return buckets
+
+
+class DecodeBuffers:
+    """Device tensors a decode step writes its metadata into.
+
+    Same names and dtypes as ``_DecodeBuffers`` (microinfer/runner.py:8-48):
+    int64 ``input_ids`` / ``positions``, int32 ``slot_mapping`` /
+    ``context_lens`` and an int32 ``block_tables [capacity, width]``. There is
+    no host mirror: the rows are written on the device.
+    """
+
+    def __init__(self, device, capacity: int = 0, width: int = 0):
+        self.device = torch.device(device)
+        self.capacity = -1
+        self.width = -1
+        self.ensure(capacity, width)
+
+    def ensure(self, batch: int, width: int) -> None:
+        if batch <= self.capacity and width <= self.width:
+            return
+        capacity, width = max(batch, self.capacity, 0), max(width, self.width, 0)
+        dev = self.device
+        self.input_ids = torch.empty(capacity, dtype=torch.int64, device=dev)
+        self.positions = torch.empty(capacity, dtype=torch.int64, device=dev)
+        self.slot_mapping = torch.empty(capacity, dtype=torch.int32, device=dev)
+        self.context_lens = torch.empty(capacity, dtype=torch.int32, device=dev)
+        self.block_tables = torch.empty((capacity, width), dtype=torch.int32, device=dev)
+        self.capacity, self.width = capacity, width
+        # Columns at or past this index are -1 in every row (a new table holds
+        # garbage everywhere).
+        self.table_written = width
+
+    def metadata(self, batch: int) -> AttentionMetadata:
+        """Decode metadata over the first ``batch`` rows (``_make_decode_metadata``,
+        microinfer/runner.py:190-197)."""
+        return AttentionMetadata.build(
+            is_prefill=False,
+            slot_mapping=self.slot_mapping[:batch],
+            context_lens=self.context_lens[:batch],
+            block_tables=self.block_tables[:batch],
+            validate_cache_write=False,
+        )
+
+
+class _Upload:
+    """Two pinned host buffers, used in turn, for the compact step description.
+
+    Before a buffer is rewritten the host waits for the copy that last read
+    it, so the host can run one step ahead of the device without racing its
+    own uploads. A description is int64 token ids followed by int32 arrays.
+    """
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.pinned = device.type == "cuda"
+        self._slots = [None, None]  # [host tensor, int64 view, int32 view, event]
+        self._turn = 0
+        self._staged = None
+
+    def stage(self, words: int):
+        """(int64, int32) numpy views of a host buffer of at least ``words``
+        int64 words that no pending copy still reads."""
+        i = self._turn
+        self._turn ^= 1
+        slot = self._slots[i]
+        if slot is None or slot[0].numel() < words:
+            size = max(words, 4096, 0 if slot is None else 2 * slot[0].numel())
+            host = torch.empty(size, dtype=torch.int64, pin_memory=self.pinned)
+            slot = [host, host.numpy(), host.view(torch.int32).numpy(), None]
+            self._slots[i] = slot
+        elif slot[3] is not None:
+            slot[3].synchronize()
+        self._staged = slot
+        return slot[1], slot[2]
+
+    def commit(self, dst: torch.Tensor, words: int) -> None:
+        """Copy the first ``words`` staged words into the int64 device tensor
+        ``dst``, asynchronously on the current stream."""
+        slot = self._staged
+        dst[:words].copy_(slot[0][:words], non_blocking=self.pinned)
+        if self.pinned:
+            if slot[3] is None:
+                slot[3] = torch.cuda.Event()
+            slot[3].record(torch.cuda.current_stream(self.device))
+
+
+class StepMetadataBuilder:
+    """Builds each step's ``(input_ids, positions, AttentionMetadata)`` on the device.
+
+    ``pad_block_id`` is the block a graph runner reserves past the scheduler's
+    pool for pad rows (``allocate_kv_cache``, microinfer/runner.py:134-153);
+    it is only needed for graph buckets.
+    """
+
+    def __init__(self, block_size: int, device, *, pad_block_id: int | None = None):
+        if block_size <= 0:
+            raise ValueError("block_size must be positive")
+        self.block_size = block_size
+        self.device = torch.device(device)
+        self.pad_block_id = pad_block_id
+        self._upload = _Upload(self.device)
+        self._decode_buffers: DecodeBuffers | None = None
+        self._decode_upload: torch.Tensor | None = None
+
+    def _check_blocks(self, last_positions: np.ndarray, counts: np.ndarray,
+                      blocks: np.ndarray) -> None:
+        """Every table covers its last scheduled position; every slot fits int32."""
+        if last_positions.size and (last_positions // self.block_size >= counts).any():
+            raise ValueError("block table does not cover scheduled tokens")
+        if blocks.size and int(blocks.max()) * self.block_size + self.block_size - 1 > _INT32_MAX:
+            raise ValueError("slot ids exceed int32")
+
+    def _launch(self, base: int, n_tok: int, layout, num_seqs, rows, num_tokens, tables,
+                table_stride, width, context_lens, slots, positions, input_ids):
+        """``layout`` = int32 word offsets (after the tokens) of cu_q, starts,
+        block offsets and blocks in the uploaded description at ``base``."""
+        at = base + 8 * n_tok
+        cu_q, starts, offsets, blocks = (at + 4 * w for w in layout)
+        self._run((cu_q, starts, offsets, blocks, base, num_seqs, rows, num_tokens,
+                   self.block_size, -1 if self.pad_block_id is None else self.pad_block_id,
+                   tables, table_stride, width, context_lens, slots, positions, input_ids))
+
+    def _run(self, args) -> None:
+        """Call ``mi_step_metadata`` with ``args`` (all but the stream)."""
+        if self.device.type != "cuda":
+            raise RuntimeError("mi_step_metadata needs a HIP device (no CPU fallback)")
+        status = _lib.load().mi_step_metadata(*args, _lib.stream_handle(self.device))
+        _lib.check(status, "mi_step_metadata")
+
+    # -- prefill --------------------------------------------------------------
+    def prepare_prefill(self, seqs):
+        """``ModelRunner.prepare_prefill`` (microinfer/runner.py:298-346) on the device."""
+        n = len(seqs)
+        starts = np.array([s.num_cached_tokens for s in seqs], dtype=np.int64)
+        counts = np.array([s.num_scheduled_tokens for s in seqs], dtype=np.int64)
+        lengths = np.array([len(s) for s in seqs], dtype=np.int64)
+        ends = starts + counts
+        if n and ((starts < 0) | (ends <= starts) | (ends > lengths)).any():
+            raise ValueError("invalid scheduled prefill range")
+        if n and max(int(ends.sum()), int(counts.sum())) > _INT32_MAX:
+            raise ValueError("scheduled tokens exceed int32")
+        tables = [s.block_table for s in seqs]
+        t_counts = np.array([len(t) for t in tables], dtype=np.int64)
+        flat = np.array(list(chain.from_iterable(tables)), dtype=np.int64)
+        self._check_blocks(ends - 1, t_counts, flat)
+        total = int(counts.sum())
+        tokens = list(chain.from_iterable(s[a:b] for s, a, b in zip(seqs, starts.tolist(),
+                                                                       ends.tolist())))
+        with_tables = bool((starts > 0).any())
+        width = int(t_counts.max()) if (with_tables and n) else 0
+
+        # int32 words after the tokens: cu_q | cu_k | starts | block offsets | blocks.
+        n32 = 4 * n + 3 + flat.size
+        words = total + (n32 + 1) // 2
+        h64, h32 = self._upload.stage(words)
+        h64[:total] = tokens
+        o = 2 * total
+        cu_q = h32[o:o + n + 1]
+        cu_k = h32[o + n + 1:o + 2 * n + 2]
+        cu_q[0] = cu_k[0] = 0
+        np.cumsum(counts, out=cu_q[1:])
+        np.cumsum(ends, out=cu_k[1:])
+        h32[o + 2 * n + 2:o + 3 * n + 2] = starts
+        h32[o + 3 * n + 2] = 0
+        np.cumsum(t_counts, out=h32[o + 3 * n + 3:o + 4 * n + 3])
+        h32[o + 4 * n + 3:o + n32] = flat
+        # One fresh device buffer: the description, then ids and positions
+        # (int64), then slots and the table (int32). Fresh per step, so the
+        # tensors returned here stay valid after later steps.
+        out_words = 2 * total + (total + n * width + 1) // 2
+        buf = torch.empty(words + out_words, dtype=torch.int64, device=self.device)
+        self._upload.commit(buf, words)
+        d32 = buf.view(torch.int32)
+        input_ids = buf[words:words + total]
+        positions = buf[words + total:words + 2 * total]
+        slots = d32[2 * (words + 2 * total):2 * (words + 2 * total) + total]
+        t0 = 2 * (words + 2 * total) + total
+        block_tables = d32[t0:t0 + n * width].view(n, width) if with_tables else None
+        if n:
+            self._launch(buf.data_ptr(), total, (0, 2 * n + 2, 3 * n + 2, 4 * n + 3), n, n,
+                         total, None if block_tables is None else block_tables.data_ptr(),
+                         width, width, None, slots.data_ptr(), positions.data_ptr(),
+                         input_ids.data_ptr())
+        metadata = AttentionMetadata.build(
+            is_prefill=True,
+            cu_seqlens_q=d32[o:o + n + 1],
+            cu_seqlens_k=d32[o + n + 1:o + 2 * n + 2],
+            max_seqlen_q=int(counts.max()) if n else 0,
+            max_seqlen_k=int(ends.max()) if n else 0,
+            slot_mapping=slots,
+            block_tables=block_tables,
+            validate_cache_write=False,
+        )
+        return input_ids, positions, metadata
+
+    # -- decode ---------------------------------------------------------------
+    def fill_decode(self, buffers: DecodeBuffers, seqs, rows: int | None = None) -> None:
+        """Write one decode row per sequence (``_fill_decode_rows``,
+        microinfer/runner.py:160-176) and, up to ``rows``, graph pad rows
+        (``_fill_graph_bucket``, :561-576) into ``buffers``."""
+        n = len(seqs)
+        rows = n if rows is None else rows
+        if rows < n or rows > buffers.capacity:
+            raise ValueError("rows must cover the batch and fit the buffers")
+        if rows > n and self.pad_block_id is None:
+            raise ValueError("pad rows need a pad block")
+        if rows and buffers.width < 1:
+            raise ValueError("decode buffers need a table width of at least 1")
+        tables = [s.block_table for s in seqs]
+        counts = np.array([len(t) for t in tables], dtype=np.int64)
+        flat = np.array(list(chain.from_iterable(tables)), dtype=np.int64)
+        lengths = np.array([len(s) for s in seqs], dtype=np.int64)
+        if n and (lengths < 1).any():
+            raise ValueError("decode sequences must be nonempty")
+        self._check_blocks(lengths - 1, counts, flat)
+        needed = int(counts.max()) if n else 0
+        if needed > buffers.width:
+            raise ValueError("block table wider than the decode buffers")
+        if rows > n:
+            needed = max(needed, 1)
+
+        # int32 words after the tokens: cu_q | starts | block offsets | blocks.
+        n32 = 3 * n + 2 + flat.size
+        words = n + (n32 + 1) // 2
+        h64, h32 = self._upload.stage(words)
+        h64[:n] = [s.last_token for s in seqs]
+        o = 2 * n
+        h32[o:o + n + 1] = np.arange(n + 1)
+        h32[o + n + 1:o + 2 * n + 1] = lengths - 1
+        h32[o + 2 * n + 1] = 0
+        np.cumsum(counts, out=h32[o + 2 * n + 2:o + 3 * n + 2])
+        h32[o + 3 * n + 2:o + n32] = flat
+        dev = self._decode_upload
+        if dev is None or dev.numel() < words:
+            dev = torch.empty(max(words, 4096), dtype=torch.int64, device=self.device)
+            self._decode_upload = dev
+        self._upload.commit(dev, words)
+        # Columns at or past buffers.table_written are -1 in every row, so only
+        # the columns a row may still hold ids in are rewritten.
+        cols = max(needed, buffers.table_written)
+        self._launch(dev.data_ptr(), n, (0, n + 1, 2 * n + 1, 3 * n + 2), n, rows, rows,
+                     buffers.block_tables.data_ptr(), buffers.width, cols,
+                     buffers.context_lens.data_ptr(), buffers.slot_mapping.data_ptr(),
+                     buffers.positions.data_ptr(), buffers.input_ids.data_ptr())
+        buffers.table_written = needed if rows == buffers.capacity else cols
+
+    def prepare_decode(self, seqs):
+        """``ModelRunner.prepare_decode`` (microinfer/runner.py:348-385) on the device.
+
+        The returned tensors are views of buffers reused by the next call,
+        as in the reference.
+        """
+        n = len(seqs)
+        width = max((len(s.block_table) for s in seqs), default=0)
+        if self._decode_buffers is None:
+            self._decode_buffers = DecodeBuffers(self.device)
+        buffers = self._decode_buffers
+        buffers.ensure(n, width)
+        if n:
+            self.fill_decode(buffers, seqs)
+        metadata = AttentionMetadata.build(
+            is_prefill=False,
+            slot_mapping=buffers.slot_mapping[:n],
+            context_lens=buffers.context_lens[:n],
+            block_tables=buffers.block_tables[:n],
+            validate_cache_write=False,
+        )
+        return buffers.input_ids[:n], buffers.positions[:n], metadata
+
+    def pad_buffers(self, batch: int, width: int) -> DecodeBuffers:
+        """Fresh bucket buffers holding only pad rows (``_fill_pad_buffers``,
+        microinfer/runner.py:203-215)."""
+        buffers = DecodeBuffers(self.device, batch, width)
+        self.fill_decode(buffers, [], rows=batch)
+        return buffers
+
+
+class DecodeGraphRunner:
+    """Graph-captured decode steps, one graph per batch bucket.
+
+    Mirrors ``capture_cuda_graphs`` / ``_capture_bucket`` / ``_run_decode``
+    (microinfer/runner.py:217-288, :555-604): each bucket has fixed buffers
+    (table width ``num_blocks + 1``, so any sequence fits), filled with pad
+    rows, warmed twice on a side stream and captured into one graph; all
+    buckets share a memory pool. ``run`` picks the smallest bucket that holds
+    the batch, writes the batch's rows and the pad rows on the device, replays
+    and returns the first ``len(seqs)`` rows of the output.
+
+    ``forward(input_ids, positions, metadata)`` is the step to capture (the
+    model's decode forward, or here the attention layers); it must be
+    capture-safe.
+    """
+
+    def __init__(self, builder: StepMetadataBuilder, forward, *, max_num_seqs: int,
+                 table_width: int):
+        if builder.pad_block_id is None:
+            raise ValueError("graph buckets need the builder's pad block")
+        if builder.device.type != "cuda":
+            raise RuntimeError("graph capture needs a HIP device")
+        self.builder = builder
+        self.forward = forward
+        self.table_width = table_width
+        self.buckets = []
+        self.pool = None
+        for batch in graph_buckets(max_num_seqs):
+            self._capture(batch)
+
+    def _capture(self, batch: int) -> None:
+        device = self.builder.device
+        buffers = self.builder.pad_buffers(batch, self.table_width)
+        ids, positions = buffers.input_ids[:batch], buffers.positions[:batch]
+        torch.cuda.synchronize(device)
+        side = torch.cuda.Stream(device=device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side), torch.inference_mode():
+            for _ in range(2):
+                self.forward(ids, positions, buffers.metadata(batch))
+        torch.cuda.current_stream(device).wait_stream(side)
+        torch.cuda.synchronize(device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, self.pool), torch.inference_mode():
+            out = self.forward(ids, positions, buffers.metadata(batch))
+        if self.pool is None:
+            self.pool = graph.pool()
+        torch.cuda.synchronize(device)
+        self.buckets.append((batch, buffers, graph, out))
+
+    def select(self, batch: int):
+        for bucket in self.buckets:
+            if bucket[0] >= batch:
+                return bucket
+        return None
+
+    def run(self, seqs):
+        """Replay the bucket that holds ``seqs``; None if the batch is larger
+        than every bucket (the caller then runs eagerly, as the reference does)."""
+        bucket = self.select(len(seqs))
+        if bucket is None:
+            return None
+        batch, buffers, graph, out = bucket
+        self.builder.fill_decode(buffers, seqs, rows=batch)
+        graph.replay()
+        return out[:len(seqs)]

@@ -131,3 +131,22 @@ def checked_paged_attention(query, key_cache, value_cache, block_tables, context
         _q_lens_cpu=tuple(q_lens),
     )
     return paged_attention_meta(query, key_cache, value_cache, metadata, scale=scale)
+
+
+class FakeSeq:
+    """The attributes of ``Sequence`` (microinfer/engine/sequence.py:14-45)
+    that the runner's metadata build reads, like the reference tests'
+    ``sequence_cls`` fixture."""
+
+    def __init__(self, token_ids):
+        self.token_ids = list(token_ids)
+        self.last_token = self.token_ids[-1]
+        self.num_cached_tokens = 0
+        self.num_scheduled_tokens = 0
+        self.block_table = []
+
+    def __len__(self):
+        return len(self.token_ids)
+
+    def __getitem__(self, key):
+        return self.token_ids[key]
