@@ -98,18 +98,24 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
   const int g = wave % G;      // query head within the group
   const int rsub = wave / G;   // 32-row sub-block of the workgroup's rows
 
-  // Request owning this query block (blocks are numbered request by request,
-  // so the blocks of one request -- which share its K/V in L2 -- run together).
+  // Request owning this query block. Requests that fit one query block
+  // (decode rows, short chunks) are numbered first: each of them is a single
+  // workgroup as long as its whole context, so started last they would form
+  // the launch's tail. The blocks of a longer request follow one another, so
+  // the workgroups sharing its K/V in L2 run together.
   const ConstI32* cu_q = (const ConstI32*)(a.cu_q);
   const ConstI32* cu_k = (const ConstI32*)(a.cu_k);
   int req = -1, qb0 = 0;
-  for (int r = 0; r < a.num_seqs; ++r) {
-    const int n = (cu_q[r + 1] - cu_q[r] + BM - 1) / BM;
-    if (qblock < qb0 + n) {
-      req = r;
-      break;
+  for (int pass = 0; pass < 2 && req < 0; ++pass) {
+    for (int r = 0; r < a.num_seqs; ++r) {
+      const int n = (cu_q[r + 1] - cu_q[r] + BM - 1) / BM;
+      if ((n == 1) != (pass == 0)) continue;
+      if (qblock < qb0 + n) {
+        req = r;
+        break;
+      }
+      qb0 += n;
     }
-    qb0 += n;
   }
   if (req < 0) return;  // surplus workgroup (uniform)
   const int q_begin = cu_q[req];
@@ -157,41 +163,54 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
     Pack<R, 8> k[kPerThread], v[kPerThread];
     int mask;  // bit h: the tile's 16-key half h has a valid block id
   };
+  // Addresses: each 16-key half of a tile lies in one cache block (block
+  // size >= 16), so its start is one scalar offset; a thread adds a constant
+  // lane offset (its key within the half, its 8-element chunk). K chunk c is
+  // key c / 16, dims (c % 16) * 8 .. +7 (16 consecutive threads read one
+  // key's 256-byte row); V chunk c is key c % 32, dims (c / 32) * 8 .. +7, so
+  // a wave's transposed LDS stores (lane = key) fall in distinct banks.
+  static_assert(kThreads % 32 == 0, "tile mapping");
+  const int64_t head_off = static_cast<int64_t>(head) * a.c_hs;
+  const int c_ts = static_cast<int>(a.c_ts);
+  int k_lane[kPerThread], v_lane[kPerThread];
+#pragma unroll
+  for (int h = 0; h < kPerThread; ++h) {
+    const int c = tid + h * kThreads;
+    k_lane[h] = ((c / 16) % 16) * c_ts + (c % 16) * 8;
+    v_lane[h] = ((c % 32) % 16) * c_ts + (c / 32) * 8;
+  }
   auto load_tile = [&](int tile, Stage& st) {
     const int t0 = tile * kKeys;
-    int ids[2] = {0, 0};
+    int64_t base[2];
     bool ok[2] = {true, true};
     if (paged) {
       const ConstI32* ctab = (const ConstI32*)(trow);
+      const int id0 = ctab[min(t0 >> a.log2_block, last_blk)];
+      const int id1 = ctab[min((t0 + 16) >> a.log2_block, last_blk)];
+      const int ids[2] = {id0, id1};
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        ids[h] = ctab[min((t0 + h * 16) >> a.log2_block, last_blk)];
         ok[h] = ids[h] >= 0 && ids[h] < a.num_blocks;
+        base[h] = static_cast<int64_t>(ok[h] ? ids[h] : 0) * a.c_bs +
+                  ((t0 + h * 16) & (a.block_size - 1)) * a.c_ts + head_off;
       }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) base[h] = (krow0 + t0 + h * 16) * a.c_ts + head_off;
     }
     st.mask = (ok[0] ? 1 : 0) | (ok[1] ? 2 : 0);
-    // Row offset of tile key `key`, or the head's first row (always in
-    // bounds; its scores are masked) when the key is past the range or in a
-    // block with an invalid id.
-    auto row_off = [&](int key) {
-      const int pos = t0 + key;
-      const int hh = key / 16;
-      const bool valid = pos < kv_end && ok[hh];
-      int64_t off;
-      if (paged)
-        off = ids[hh] * a.c_bs + (pos & (a.block_size - 1)) * a.c_ts;
-      else
-        off = (krow0 + pos) * a.c_ts;
-      return valid ? off + head * a.c_hs : head * a.c_hs;
-    };
+    // Keys past the range or in a block with an invalid id read the head's
+    // first row instead (always in bounds; their scores are masked).
 #pragma unroll
     for (int h = 0; h < kPerThread; ++h) {
-      // K: 16 consecutive threads read one key's 256-byte row (coalesced).
       const int c = tid + h * kThreads;
-      st.k[h] = load_pack<R, 8>(kc + row_off(c / 16) + (c % 16) * 8);
-      // V: a wave's lanes take 32 keys x 2 column chunks, so its transposed
-      // LDS stores (lane = key) fall in distinct banks.
-      st.v[h] = load_pack<R, 8>(vc + row_off(c % 32) + (c / 32) * 8);
+      const int kk = c / 16, vk = c % 32;
+      const bool k_valid = t0 + kk < kv_end && ok[kk / 16];
+      const bool v_valid = t0 + vk < kv_end && ok[vk / 16];
+      const int64_t kb = kk / 16 ? base[1] : base[0];
+      const int64_t vb = vk / 16 ? base[1] : base[0];
+      st.k[h] = load_pack<R, 8>(kc + (k_valid ? kb + k_lane[h] : head_off + (c % 16) * 8));
+      st.v[h] = load_pack<R, 8>(vc + (v_valid ? vb + v_lane[h] : head_off + (c / 32) * 8));
     }
   };
   auto store_tile = [&](int buf, const Stage& st) {
@@ -217,24 +236,16 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
   // One 32-key tile from LDS buffer `buf`.
   auto compute = [&](int tile, int buf, int mask) {
     // S^T = K . Q^T: s[i] is key (i/4)*8 + half*4 + i%4 of this lane's row.
-    // Two independent accumulation chains (head dims 0-63 and 64-127) keep
-    // the MFMA pipeline fed; they are summed once.
-    f32x16_t s, s2;
+    // One accumulation chain: a dependent MFMA takes its accumulator
+    // straight from the previous one, so a chain issues as fast as
+    // independent MFMAs would.
+    f32x16_t s;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      s[i] = 0.f;
-      s2[i] = 0.f;
-    }
+    for (int i = 0; i < 16; ++i) s[i] = 0.f;
     const R* krow = &s_k[buf][col * kKStride + half * 8];
 #pragma unroll
-    for (int ks = 0; ks < kD / 32; ++ks) {
-      const vec8 k0 = __builtin_bit_cast(vec8, load_pack<R, 8>(krow + ks * 16));
-      const vec8 k1 = __builtin_bit_cast(vec8, load_pack<R, 8>(krow + (ks + kD / 32) * 16));
-      s = M::mma(k0, qf[ks], s);
-      s2 = M::mma(k1, qf[ks + kD / 32], s2);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] += s2[i];
+    for (int ks = 0; ks < kD / 16; ++ks)
+      s = M::mma(__builtin_bit_cast(vec8, load_pack<R, 8>(krow + ks * 16)), qf[ks], s);
 
     // Mask (causal, past the workgroup's keys, invalid blocks) only where the
     // tile reaches one of those limits for some row of the wave; interior
@@ -320,31 +331,35 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
   // tile t + 2 into set t % 2 and stores set (t + 1) % 2 (tile t + 1) into
   // buffer (t + 1) % 2. Loads past the last tile re-read the last tile and
   // are never stored.
-  Stage st0, st1;
-  int mb0 = 0, mb1 = 0;  // masks of the tiles held in LDS buffers 0 and 1
+  // The loop sits inside the prologue's branch so that every path into it
+  // has passed the prologue's waits: the compiler's wait insertion is static,
+  // and a path that skipped them would make it wait for all loads (the
+  // prefetched tiles included) at the top of every iteration.
   if (ntiles > 0) {
+    Stage st0, st1;
+    int mb0 = 0, mb1 = 0;  // masks of the tiles held in LDS buffers 0 and 1
     load_tile(0, st0);
     load_tile(min(1, ntiles - 1), st1);
     store_tile(0, st0);
     mb0 = st0.mask;
-  }
-  __syncthreads();
-  for (int t = 0; t < ntiles; t += 2) {
-    load_tile(min(t + 2, ntiles - 1), st0);
-    compute(t, 0, mb0);
-    if (t + 1 < ntiles) {
-      store_tile(1, st1);
-      mb1 = st1.mask;
-    }
     __syncthreads();
-    if (t + 1 >= ntiles) break;
-    load_tile(min(t + 3, ntiles - 1), st1);
-    compute(t + 1, 1, mb1);
-    if (t + 2 < ntiles) {
-      store_tile(0, st0);
-      mb0 = st0.mask;
+    for (int t = 0; t < ntiles; t += 2) {
+      load_tile(min(t + 2, ntiles - 1), st0);
+      compute(t, 0, mb0);
+      if (t + 1 < ntiles) {
+        store_tile(1, st1);
+        mb1 = st1.mask;
+      }
+      __syncthreads();
+      if (t + 1 >= ntiles) break;
+      load_tile(min(t + 3, ntiles - 1), st1);
+      compute(t + 1, 1, mb1);
+      if (t + 2 < ntiles) {
+        store_tile(0, st0);
+        mb0 = st0.mask;
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
 
   // o[db][i] = O^T[d = db*32 + (i/4)*8 + half*4 + i%4][row].
@@ -386,7 +401,8 @@ int32_t launch_typed(const AttnArgs& a, hipStream_t stream) {
 bool prefill_mfma_supported(const AttnArgs& a, int32_t dtype) {
   return (dtype == MI_DTYPE_BF16 || dtype == MI_DTYPE_F16) && a.head_dim == kD &&
          (a.group == 1 || a.group == 2 || a.group == 4) &&
-         (a.tables == nullptr || a.block_size >= 16);
+         (a.tables == nullptr || a.block_size >= 16) && a.c_ts >= 0 &&
+         a.c_ts < (int64_t(1) << 26);  // lane offsets (< 16 rows) stay in int32
 }
 
 int32_t launch_prefill_mfma(const AttnArgs& a, int32_t dtype, hipStream_t stream) {
