@@ -56,6 +56,20 @@ def blas_threads() -> int:
         return 1
 
 
+def warm_up(torch, run, args) -> None:
+    """The W untimed warmup steps, continued (still untimed) until at least
+    --warmup-seconds have passed: the GPU's clocks take about a second of
+    sustained work to settle, and a timed region that starts cold measures
+    the ramp instead of the kernels."""
+    t_end = time.perf_counter() + args.warmup_seconds
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    while time.perf_counter() < t_end:
+        run()
+        torch.cuda.synchronize()
+
+
 def build_decode_state(torch, layers: int, layout: str):
     from microinfer_amd.workloads import QWEN3_06B, make_decode_batch
     from microinfer_amd.worker.kv_cache import KVCache
@@ -87,15 +101,16 @@ def build_decode_state(torch, layers: int, layout: str):
     )
 
 
-TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                               "paged_decode_traffic_qwen3-0.6b_b32.json")
+PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+DECODE_TRAFFIC = os.path.join(PROFILES, "paged_decode_traffic_qwen3-0.6b_b32.json")
+PREFILL_TRAFFIC = os.path.join(PROFILES, "paged_prefill_traffic_qwen3-8b_mixed.json")
 
 
-def measured_traffic():
-    """HBM bytes per decode launch from the committed FETCH_SIZE / WRITE_SIZE runs
+def measured_traffic(path: str):
+    """HBM bytes per launch from a committed FETCH_SIZE / WRITE_SIZE summary
     (calibrated against a copy kernel), or None when that profile is absent."""
     try:
-        with open(TRAFFIC_PROFILE) as f:
+        with open(path) as f:
             return int(json.load(f)["traffic_bytes_per_launch"])
     except (OSError, KeyError, ValueError):
         return None
@@ -227,24 +242,26 @@ def run_prefill(args) -> int:
     cu_k = torch.tensor(batch.cu_seqlens_k, device=dev)
     max_q = int(batch.q_lens.max())
     scale = 1 / math.sqrt(128)
-    out = torch.empty_like(q)
 
     def step():
-        out.copy_(hip_paged_prefill(q, cache.keys[0], cache.values[0], cu_q, cu_k, tables,
-                                    max_seqlen_q=max_q, scale=scale))
+        # The output is allocated by the call (from the graph's pool when
+        # captured); the step is the launch alone.
+        return hip_paged_prefill(q, cache.keys[0], cache.values[0], cu_q, cu_k, tables,
+                                 max_seqlen_q=max_q, scale=scale)
 
     step()
     torch.cuda.synchronize()
-    if args.no_graph:
-        run = step
-    else:
+    # A step is one launch: launched eagerly, back to back, the launches queue
+    # behind each other and the events time the kernels; a graph replay per
+    # launch would add its own gap (--graph measures that).
+    if args.graph:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             step()
         run = graph.replay
-    for _ in range(args.warmup):
-        run()
-    torch.cuda.synchronize()
+    else:
+        run = step
+    warm_up(torch, run, args)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(args.steps):
@@ -252,6 +269,8 @@ def run_prefill(args) -> int:
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
+    if args.copy_calibration_mib:
+        copy_calibration(torch, args.copy_calibration_mib)
     flops = prefill_flops(batch.q_lens, batch.context_lens, num_q_heads=32, head_dim=128)
     tflops = flops / (ms * 1e-3) / 1e12
     log(f"{ms * 1e3:.1f} us per launch, {tflops:.1f} TFLOP/s")
@@ -262,6 +281,7 @@ def run_prefill(args) -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_seconds": args.warmup_seconds,
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -273,7 +293,7 @@ def run_prefill(args) -> int:
                          "head_dim 128), bf16, block 16, pool 65536 blocks: 8 chunks of 512 "
                          "rows on prefixes U[0,3072] (first 1024 tokens shared) + 24 decode "
                          "rows with contexts U[256,2048] (seed 0), one varlen launch per step, "
-                         + ("launched eagerly" if args.no_graph else "hipGraph replay")),
+                         + ("hipGraph replay" if args.graph else "launched eagerly back to back")),
             "query_rows": total_q,
             "flops_per_launch": flops,
             "kv_layout": args.layout,
@@ -284,7 +304,7 @@ def run_prefill(args) -> int:
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(PREFILL_TRAFFIC),
             "kernel": "paged_prefill_mfma_kernel",
             "flops_per_launch": flops,
             "us_per_launch": round(ms * 1e3, 3),
@@ -402,6 +422,7 @@ def run_step_metadata(args) -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_seconds": args.warmup_seconds,
         "ms_per_step": round(us_per_step / 1e3, 5),
         "higher_is_better": False,
         "scaling": "weak",
@@ -479,6 +500,8 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--warmup-seconds", type=float, default=1.0,
+                        help="keep running untimed warmup steps until this long has passed")
     parser.add_argument("--layers", type=int, default=28)
     parser.add_argument("--layout", default="head_major", choices=["head_major", "token_major"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -488,7 +511,9 @@ def main() -> int:
                              "chunked-prefill (MFMA) line; step-metadata: the decode step's "
                              "device-built metadata")
     parser.add_argument("--no-graph", action="store_true",
-                        help="launch the step eagerly (for per-dispatch counter runs)")
+                        help="decode: launch the step eagerly (for per-dispatch counter runs)")
+    parser.add_argument("--graph", action="store_true",
+                        help="prefill: replay the one-launch step from a hipGraph")
     parser.add_argument("--copy-calibration-mib", type=int, default=0,
                         help="after timing, run one device copy of this many MiB (the "
                              "known-size kernel that scales FETCH_SIZE / WRITE_SIZE)")
@@ -535,15 +560,21 @@ def main() -> int:
         run = step
     else:
         log("capturing the decode step in a hipGraph")
+        # One eager step on the capture stream first: the library keeps a
+        # zeroed arrival-counter array per stream, and allocating it here
+        # keeps its zero fill out of the graph.
+        capture_stream = torch.cuda.Stream()
+        capture_stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(capture_stream):
+            step()
+        torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        with torch.cuda.graph(graph, stream=capture_stream):
             step()
         torch.cuda.synchronize()
         run = graph.replay
 
-    for _ in range(args.warmup):
-        run()
-    torch.cuda.synchronize()
+    warm_up(torch, run, args)
     # Events on torch's current stream, which is the stream every launch of
     # the step goes to (the library reads it at call time).
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -575,6 +606,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_seconds": args.warmup_seconds,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -598,7 +630,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(),
+            "traffic": measured_traffic(DECODE_TRAFFIC),
             "kernel": "paged_attention_vector_kernel (fused append + decode + split merge)",
             "bytes_per_launch": layer_bytes,
             "us_per_launch": round(layer_us, 3),

@@ -15,10 +15,14 @@
 //    online softmax needs one cross-lane exchange per statistic.
 //  * O^T += V^T . P^T on the same instruction: P^T comes straight from the
 //    softmax registers. The MFMA reduction index is mapped to keys the way
-//    the S^T result lays them out, and V is stored transposed in LDS with the
-//    same mapping, so no shuffles of P are needed.
-//  * K/V tiles are double-buffered in LDS; the next tile's global loads are in
-//    flight while the current tile is computed. One barrier per tile.
+//    the S^T result lays them out; the V^T fragments are read from the
+//    row-major V tile with transposing LDS reads (ds_read_b64_tr_b16), so
+//    neither P nor V is shuffled.
+//  * K/V tiles move from global memory straight into LDS
+//    (global_load_lds_dwordx4: no staging registers, no LDS store
+//    instructions) through three LDS buffers, two tiles ahead of the one being
+//    computed. One barrier per tile; 158 VGPRs, so three workgroups (12 waves)
+//    share a CU.
 #include "paged_attention.h"
 
 namespace mi {
@@ -49,6 +53,10 @@ __device__ __forceinline__ float partner32(float v, int lane) {
   return __builtin_bit_cast(float, lane < 32 ? r[1] : r[0]);
 }
 
+// Two packed 1.0 values of the element type (for row sums with dot2).
+template <typename E>
+constexpr uint32_t kOnes2 = std::is_same<E, BF16>::value ? 0x3F803F80u : 0x3C003C00u;
+
 template <typename E>
 struct Mfma;
 template <>
@@ -69,24 +77,65 @@ struct Mfma<F16> {
 constexpr int kD = 128;               // head_dim
 constexpr int kKeys = 32;             // keys per tile
 constexpr int kRows = 32;             // query rows per wave (MFMA N)
-#ifndef MI_PREFILL_WAVES
-#define MI_PREFILL_WAVES 4
-#endif
-constexpr int kWaves = MI_PREFILL_WAVES;  // waves per workgroup
+constexpr int kWaves = 4;             // waves per workgroup
 constexpr int kThreads = kWaves * kWave;
-constexpr int kKStride = kD + 8;      // K tile row stride in LDS (elements)
-constexpr int kVStride = kKeys + 4;   // V^T tile row stride in LDS (elements)
-constexpr int kPerThread = kKeys * kD / 8 / kThreads;  // 16-byte chunks per thread
+constexpr int kTileElems = kKeys * kD;  // one K or V tile in LDS (8 KiB of bf16)
+// Rows of a tile each wave moves with direct global->LDS loads (4 rows of
+// 256 bytes per instruction).
+constexpr int kRowsPerWave = kKeys / kWaves;
+static_assert(kWaves == 4 && kRowsPerWave % 4 == 0, "tile load mapping");
+
+// LDS tile layout: key rows of 256 bytes (all 64 banks), row-major, with the
+// 16-byte chunk c of key k stored at position c ^ swz(k). LDS serves 256
+// bytes per clock, so an access is conflict-free when each group of lanes
+// served together covers 256 distinct bytes:
+//  * K fragment reads (16 lanes x 16 bytes: keys k..k+15, one logical chunk)
+//    need 16 distinct positions: swz_k(k) = k & 15.
+//  * Transposed V reads (32 lanes x 8 bytes: 4 consecutive keys x 4 aligned
+//    chunks) need the 4 keys' chunk groups disjoint: swz_v(k) = 4 * (k & 3).
+__device__ __forceinline__ int swz_k(int key) { return key & 15; }
+__device__ __forceinline__ int swz_v(int key) { return 4 * (key & 3); }
+
+// Largest exponent a probability may reach before the running maximum is
+// moved (p <= 2^15 fits f16 as well as bf16).
+constexpr float kRescaleSlack = 15.f;
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+using LdsShort4 = __attribute__((address_space(3))) short4_t;
+using LdsVoid = __attribute__((address_space(3))) void;
+
+// Direct global->LDS load of 16 bytes per lane: lane i's bytes land at
+// lds_dst + 16 i (global_load_lds_dwordx4, LDS base in M0; one wait state
+// between the M0 write and the load). Issued as inline assembly so that the
+// compiler does not track it: its own wait insertion would otherwise wait for
+// these loads before every LDS read. The kernel waits for them explicitly
+// (vmcnt) and orders them with bare barriers.
+__device__ __forceinline__ void lds_load16(const void* src, const void* lds_dst) {
+  const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (const __attribute__((address_space(3))) void*)(lds_dst)));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds)
+               : "memory", "m0");
+}
+
+// Four 16-bit elements, transposed across each group of 16 lanes
+// (ds_read_b64_tr_b16): lane l of a group receives element l % 4 of the
+// 8-byte rows read by lanes l / 4, l / 4 + 4, l / 4 + 8 and l / 4 + 12.
+__device__ __forceinline__ short4_t read_tr(const uint16_t* lds_elem) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsShort4*)(lds_elem));
+}
 
 template <typename E, int G>
-__global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(kThreads, 3) void paged_prefill_mfma_kernel(const AttnArgs a) {
   using M = Mfma<E>;
   using vec8 = typename M::vec8;
   using R = uint16_t;
   constexpr int BM = kRows * kWaves / G;  // query rows per workgroup
   using ConstI32 = __attribute__((address_space(4))) const int32_t;
-  __shared__ __attribute__((aligned(16))) R s_k[2][kKeys * kKStride];
-  __shared__ __attribute__((aligned(16))) R s_vt[2][kD * kVStride];
+  // Three K/V tile buffers (48 KiB per workgroup).
+  __shared__ __attribute__((aligned(16))) R s_k[3][kTileElems];
+  __shared__ __attribute__((aligned(16))) R s_v[3][kTileElems];
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
@@ -143,43 +192,38 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
   // this lane supplies dims ks*16 + half*8 .. +7 of its row.
   const R* qrow = static_cast<const R*>(a.q) + (q_begin + my_row) * a.q_ts +
                   (head * G + g) * a.q_hs;
+  // Loaded after the first tiles' loads are issued (their latencies overlap);
+  // an explicit full wait then leaves the compiler no Q load to wait for
+  // inside the loop, where it would also wait for the prefetched tiles.
   vec8 qf[kD / 16];
-#pragma unroll
-  for (int ks = 0; ks < kD / 16; ++ks) {
-    Pack<R, 8> p = zero_pack<R, 8>();
-    if (row_ok) p = load_pack<R, 8>(qrow + ks * 16 + half * 8);
-    qf[ks] = __builtin_bit_cast(vec8, p);
-  }
 
-  // Tile loads: thread t moves chunks t and t + 256 of K and of V (key c / 16,
-  // dims (c % 16) * 8 .. +7), i.e. one key from each 16-key half of the tile.
+  // Tile loads go straight from global memory to LDS
+  // (global_load_lds_dwordx4: lane i of an instruction writes bytes
+  // 16i .. 16i+15 after the instruction's LDS base). Wave w moves key rows
+  // 8w .. 8w+7 of the tile, four per instruction: lane i takes row
+  // R + i / 16 and LDS chunk position i % 16, i.e. logical chunk
+  // (i % 16) ^ swz(row). Each 16-key half of a tile lies in one cache block
+  // (block size >= 16), so an instruction's rows share one scalar base and
+  // each lane adds a constant offset.
   const R* kc = static_cast<const R*>(a.kc);
   const R* vc = static_cast<const R*>(a.vc);
   const int32_t* trow = paged ? a.tables + req * a.t_stride : nullptr;
   const int last_blk = max((kv_end - 1) >> a.log2_block, 0);
-  // Two register sets: the loads of tile t are issued two tiles ahead (at
-  // the start of tile t - 2) and written to LDS at the end of tile t - 1.
-  struct Stage {
-    Pack<R, 8> k[kPerThread], v[kPerThread];
-    int mask;  // bit h: the tile's 16-key half h has a valid block id
-  };
-  // Addresses: each 16-key half of a tile lies in one cache block (block
-  // size >= 16), so its start is one scalar offset; a thread adds a constant
-  // lane offset (its key within the half, its 8-element chunk). K chunk c is
-  // key c / 16, dims (c % 16) * 8 .. +7 (16 consecutive threads read one
-  // key's 256-byte row); V chunk c is key c % 32, dims (c / 32) * 8 .. +7, so
-  // a wave's transposed LDS stores (lane = key) fall in distinct banks.
-  static_assert(kThreads % 32 == 0, "tile mapping");
   const int64_t head_off = static_cast<int64_t>(head) * a.c_hs;
   const int c_ts = static_cast<int>(a.c_ts);
-  int k_lane[kPerThread], v_lane[kPerThread];
+  // This wave's rows all lie in one 16-key half of the tile.
+  const bool wave_half = wave * kRowsPerWave >= 16;
+  int ld_key[kRowsPerWave / 4], ld_k[kRowsPerWave / 4], ld_v[kRowsPerWave / 4];
 #pragma unroll
-  for (int h = 0; h < kPerThread; ++h) {
-    const int c = tid + h * kThreads;
-    k_lane[h] = ((c / 16) % 16) * c_ts + (c % 16) * 8;
-    v_lane[h] = ((c % 32) % 16) * c_ts + (c / 32) * 8;
+  for (int i = 0; i < kRowsPerWave / 4; ++i) {
+    const int key = wave * kRowsPerWave + 4 * i + lane / 16;
+    ld_key[i] = key;
+    ld_k[i] = ((lane % 16) ^ swz_k(key)) * 8;  // logical chunk offsets (elements)
+    ld_v[i] = ((lane % 16) ^ swz_v(key)) * 8;
   }
-  auto load_tile = [&](int tile, Stage& st) {
+  // Issue the loads of `tile` into (kbuf, vbuf); returns the tile's mask
+  // (bit h: its 16-key half h has a valid block id).
+  auto issue_tile = [&](int tile, R* kbuf, R* vbuf) {
     const int t0 = tile * kKeys;
     int64_t base[2];
     bool ok[2] = {true, true};
@@ -198,32 +242,41 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
 #pragma unroll
       for (int h = 0; h < 2; ++h) base[h] = (krow0 + t0 + h * 16) * a.c_ts + head_off;
     }
-    st.mask = (ok[0] ? 1 : 0) | (ok[1] ? 2 : 0);
-    // Keys past the range or in a block with an invalid id read the head's
-    // first row instead (always in bounds; their scores are masked).
+    const int64_t wbase = wave_half ? base[1] : base[0];
+    const bool wok = wave_half ? ok[1] : ok[0];
 #pragma unroll
-    for (int h = 0; h < kPerThread; ++h) {
-      const int c = tid + h * kThreads;
-      const int kk = c / 16, vk = c % 32;
-      const bool k_valid = t0 + kk < kv_end && ok[kk / 16];
-      const bool v_valid = t0 + vk < kv_end && ok[vk / 16];
-      const int64_t kb = kk / 16 ? base[1] : base[0];
-      const int64_t vb = vk / 16 ? base[1] : base[0];
-      st.k[h] = load_pack<R, 8>(kc + (k_valid ? kb + k_lane[h] : head_off + (c % 16) * 8));
-      st.v[h] = load_pack<R, 8>(vc + (v_valid ? vb + v_lane[h] : head_off + (c / 32) * 8));
+    for (int i = 0; i < kRowsPerWave / 4; ++i) {
+      const int row0 = wave * kRowsPerWave + 4 * i;  // wave-uniform
+      // Keys past the range or in a block with an invalid id read the head's
+      // first row instead (always in bounds; their scores are masked).
+      const bool valid = wok && t0 + ld_key[i] < kv_end;
+      const int64_t row = valid ? wbase + (ld_key[i] % 16) * c_ts : head_off;
+      lds_load16(kc + row + ld_k[i], kbuf + row0 * kD);
+      lds_load16(vc + row + ld_v[i], vbuf + row0 * kD);
     }
+    return (ok[0] ? 1 : 0) | (ok[1] ? 2 : 0);
   };
-  auto store_tile = [&](int buf, const Stage& st) {
+
+  // Per-lane LDS element offsets of the fragment reads.
+  // K (A operand of S^T): lane reads key `col`, logical chunk 2*ks + half,
+  // stored at element col*128 + 8*((2*ks + half) ^ (col & 15)) =
+  // col*128 + ((16*ks) ^ k_x) with k_x = 8*((col & 15) ^ half).
+  const int k_rd0 = col * kD;
+  const int k_x = 8 * (swz_k(col) ^ half);
+  // V^T (A operand of O^T), read transposed: lane (group gq = lane / 16,
+  // s = lane % 16) supplies the 8-byte row of key 16c + 8j + (gq/2)*4 + s/4 at
+  // dims db*32 + (gq%2)*16 + 4*(s%4); after the transpose, lane gets
+  // V[16c + 8j + half*4 + k][db*32 + col] in element k.
+  int v_rd[kD / 32];
+  {
+    const int gq = lane / 16, sl = lane % 16;
+    const int vkey = (gq / 2) * 4 + sl / 4;  // row within each 8-key group
 #pragma unroll
-    for (int h = 0; h < kPerThread; ++h) {
-      const int c = tid + h * kThreads;
-      store_pack<R, 8>(&s_k[buf][(c / 16) * kKStride + (c % 16) * 8], st.k[h]);
-      const int key = c % 32;
-      const int d0 = (c / 32) * 8;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) s_vt[buf][(d0 + j) * kVStride + key] = st.v[h].v[j];
+    for (int db = 0; db < kD / 32; ++db) {
+      const int chunk = 4 * db + 2 * (gq % 2) + (sl % 4) / 2;
+      v_rd[db] = vkey * kD + ((chunk ^ swz_v(vkey)) * 8) + 4 * (sl % 2);
     }
-  };
+  }
 
   f32x16_t o[kD / 32];
 #pragma unroll
@@ -233,8 +286,8 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
   float m = -INFINITY, l = 0.f;
   const float scale_log2 = a.scale_log2;
 
-  // One 32-key tile from LDS buffer `buf`.
-  auto compute = [&](int tile, int buf, int mask) {
+  // One 32-key tile from LDS buffers (kbuf, vbuf).
+  auto compute = [&](int tile, const R* kbuf, const R* vbuf, int mask) {
     // S^T = K . Q^T: s[i] is key (i/4)*8 + half*4 + i%4 of this lane's row.
     // One accumulation chain: a dependent MFMA takes its accumulator
     // straight from the previous one, so a chain issues as fast as
@@ -242,10 +295,9 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
     f32x16_t s;
 #pragma unroll
     for (int i = 0; i < 16; ++i) s[i] = 0.f;
-    const R* krow = &s_k[buf][col * kKStride + half * 8];
 #pragma unroll
     for (int ks = 0; ks < kD / 16; ++ks)
-      s = M::mma(__builtin_bit_cast(vec8, load_pack<R, 8>(krow + ks * 16)), qf[ks], s);
+      s = M::mma(__builtin_bit_cast(vec8, load_pack<R, 8>(kbuf + k_rd0 + ((16 * ks) ^ k_x))), qf[ks], s);
 
     // Mask (causal, past the workgroup's keys, invalid blocks) only where the
     // tile reaches one of those limits for some row of the wave; interior
@@ -270,10 +322,11 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
     // Online softmax in the log2 domain on scaled scores s * c (c > 0, so the
     // maximum can be taken on raw scores). The running maximum m is moved --
     // and O and l rescaled -- only when some row's tile maximum exceeds it by
-    // more than 8, a wave-uniform decision; otherwise exponents stay below
-    // 2^8 and the normalisation by l at the end is unchanged.
+    // more than kRescaleSlack, a wave-uniform decision; otherwise exponents
+    // stay below 2^kRescaleSlack and the normalisation by l at the end is
+    // unchanged.
     smax = fmaxf(smax, partner32(smax, lane)) * scale_log2;
-    if (__ballot(smax > m + 8.f) != 0) {
+    if (__ballot(smax > m + kRescaleSlack) != 0) {
       const float mnew = fmaxf(m, smax);
       const float alpha = (mnew == -INFINITY) ? 1.f : fast_exp2(m - mnew);
       l *= alpha;
@@ -285,80 +338,88 @@ __global__ __launch_bounds__(kThreads, 2) void paged_prefill_mfma_kernel(const A
     }
     const float neg_m = m == -INFINITY ? 0.f : -m;  // all scores masked so far: p = 0
     float p[16];
-    float rs = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      p[i] = fast_exp2(fmaf(s[i], scale_log2, neg_m));
-      rs += p[i];
-    }
-    // Same sum on both halves: lower half adds (own, partner), upper half
-    // (partner, own), i.e. always (lane l & 31) + (lane l | 32).
-    const float other = partner32(rs, lane);
-    l += lane < 32 ? rs + other : other + rs;
+    for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(s[i], scale_log2, neg_m));
 
     // P^T fragments: reduction slot j of 16-key chunk c is this lane's
-    // p[8c + j], i.e. key 16c + (j/4)*8 + half*4 + j%4.
+    // p[8c + j], i.e. key 16c + (j/4)*8 + half*4 + j%4. The row sum is taken
+    // over the rounded 16-bit values (the weights the MFMA applies), two per
+    // dot2 instruction.
     vec8 pf[2];
+    float rs = 0.f;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       Pack<R, 8> pk;
 #pragma unroll
       for (int j = 0; j < 8; ++j) pk.v[j] = to_raw<E>(p[8 * c + j]);
       pf[c] = __builtin_bit_cast(vec8, pk);
+      const Pack<uint32_t, 4> w = __builtin_bit_cast(Pack<uint32_t, 4>, pk);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rs = E::dot2(w.v[j], kOnes2<E>, rs);
     }
-    // O^T += V^T . P^T with the same key mapping on the A side: lane reads
-    // V^T[d][16c + half*4 .. +3] and V^T[d][16c + 8 + half*4 .. +3].
+    // Same sum on both halves: lower half adds (own, partner), upper half
+    // (partner, own), i.e. always (lane l & 31) + (lane l | 32).
+    const float other = partner32(rs, lane);
+    l += lane < 32 ? rs + other : other + rs;
+    // O^T += V^T . P^T with the same key mapping on the A side: slots 0-3
+    // of chunk c hold keys 16c + half*4 .. +3, slots 4-7 keys 16c + 8 +
+    // half*4 .. +3 (two transposed reads, 8 keys apart).
 #pragma unroll
     for (int db = 0; db < kD / 32; ++db) {
-      const R* vrow = &s_vt[buf][(db * 32 + col) * kVStride + half * 4];
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const Pack<R, 4> lo = load_pack<R, 4>(vrow + 16 * c);
-        const Pack<R, 4> hi = load_pack<R, 4>(vrow + 16 * c + 8);
-        Pack<R, 8> vv;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          vv.v[j] = lo.v[j];
-          vv.v[4 + j] = hi.v[j];
-        }
-        o[db] = M::mma(__builtin_bit_cast(vec8, vv), pf[c], o[db]);
+        const short4_t lo = read_tr(vbuf + v_rd[db] + (16 * c) * kD);
+        const short4_t hi = read_tr(vbuf + v_rd[db] + (16 * c + 8) * kD);
+        const short4_t both[2] = {lo, hi};
+        o[db] = M::mma(__builtin_bit_cast(vec8, both), pf[c], o[db]);
       }
     }
   };
 
-  // Pipeline, unrolled by two so each register set and LDS buffer has a
-  // fixed role: step t computes tile t from buffer t % 2, issues the loads of
-  // tile t + 2 into set t % 2 and stores set (t + 1) % 2 (tile t + 1) into
-  // buffer (t + 1) % 2. Loads past the last tile re-read the last tile and
-  // are never stored.
+  // Pipeline over three LDS buffers, unrolled by three so each buffer has a
+  // fixed role. Step t: wait for this wave's loads of tile t, barrier (every
+  // wave's tile t is in LDS and every wave is done with tile t - 1), issue
+  // tile t + 2 into the buffer tile t - 1 used, compute tile t.
   // The loop sits inside the prologue's branch so that every path into it
-  // has passed the prologue's waits: the compiler's wait insertion is static,
-  // and a path that skipped them would make it wait for all loads (the
-  // prefetched tiles included) at the top of every iteration.
+  // has passed the prologue (the compiler's wait insertion is static).
+  auto wait_tile = [&](bool next_in_flight) {
+    // vmcnt(4) leaves the next tile's four loads in flight; vmcnt(0) waits
+    // for everything (s_waitcnt encoding: vmcnt in bits 3:0, expcnt 6:4 = 7
+    // (no wait), lgkmcnt 11:8).
+    // lgkmcnt(0): this wave's reads of the buffer about to be refilled have
+    // returned. The barrier is a bare s_barrier: __syncthreads() would add a
+    // release fence that waits for every load in flight.
+    if (next_in_flight)
+      __builtin_amdgcn_s_waitcnt(0x0074);
+    else
+      __builtin_amdgcn_s_waitcnt(0x0070);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  };
+  static_assert(kRowsPerWave / 4 * 2 == 4, "vmcnt above assumes four loads per wave per tile");
   if (ntiles > 0) {
-    Stage st0, st1;
-    int mb0 = 0, mb1 = 0;  // masks of the tiles held in LDS buffers 0 and 1
-    load_tile(0, st0);
-    load_tile(min(1, ntiles - 1), st1);
-    store_tile(0, st0);
-    mb0 = st0.mask;
-    __syncthreads();
-    for (int t = 0; t < ntiles; t += 2) {
-      load_tile(min(t + 2, ntiles - 1), st0);
-      compute(t, 0, mb0);
-      if (t + 1 < ntiles) {
-        store_tile(1, st1);
-        mb1 = st1.mask;
-      }
-      __syncthreads();
-      if (t + 1 >= ntiles) break;
-      load_tile(min(t + 3, ntiles - 1), st1);
-      compute(t + 1, 1, mb1);
+    int mask[3] = {0, 0, 0};
+    mask[0] = issue_tile(0, s_k[0], s_v[0]);
+    if (ntiles > 1) mask[1] = issue_tile(1, s_k[1], s_v[1]);
+#pragma unroll
+    for (int ks = 0; ks < kD / 16; ++ks) {
+      Pack<R, 8> p = zero_pack<R, 8>();
+      if (row_ok) p = load_pack<R, 8>(qrow + ks * 16 + half * 8);
+      qf[ks] = __builtin_bit_cast(vec8, p);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+    int cur = 0;
+    for (int t = 0; t < ntiles; ++t) {
+      wait_tile(t + 1 < ntiles);
+      const int nxt = cur == 0 ? 2 : cur - 1;  // (t + 2) % 3
+      const int mcur = cur == 0 ? mask[0] : (cur == 1 ? mask[1] : mask[2]);
       if (t + 2 < ntiles) {
-        store_tile(0, st0);
-        mb0 = st0.mask;
+        const int m2 = issue_tile(t + 2, s_k[nxt], s_v[nxt]);
+        if (nxt == 0) mask[0] = m2; else if (nxt == 1) mask[1] = m2; else mask[2] = m2;
       }
-      __syncthreads();
+      compute(t, s_k[cur], s_v[cur], mcur);
+      cur = cur == 2 ? 0 : cur + 1;
     }
   }
 

@@ -364,7 +364,10 @@ class DecodeGraphRunner:
         torch.cuda.current_stream(device).wait_stream(side)
         torch.cuda.synchronize(device)
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, self.pool), torch.inference_mode():
+        # Captured on the warm-up stream, so per-stream state the library
+        # created during the warm-up (the decode arrival counters) is reused
+        # rather than allocated and zero-filled inside the graph.
+        with torch.cuda.graph(graph, self.pool, stream=side), torch.inference_mode():
             out = self.forward(ids, positions, buffers.metadata(batch))
         if self.pool is None:
             self.pool = graph.pool()
