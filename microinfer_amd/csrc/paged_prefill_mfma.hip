@@ -126,7 +126,11 @@ __device__ __forceinline__ short4_t read_tr(const uint16_t* lds_elem) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsShort4*)(lds_elem));
 }
 
-template <typename E, int G>
+// A32: every element offset into the caches fits in int32 (checked on the
+// host), so tile bases are computed with 32-bit scalar arithmetic; the
+// per-tile 64-bit multiplies otherwise cost about 4 % of the kernel in scalar
+// issue slots.
+template <typename E, int G, bool A32>
 __global__ __launch_bounds__(kThreads, 3) void paged_prefill_mfma_kernel(const AttnArgs a) {
   using M = Mfma<E>;
   using vec8 = typename M::vec8;
@@ -211,6 +215,8 @@ __global__ __launch_bounds__(kThreads, 3) void paged_prefill_mfma_kernel(const A
   const int last_blk = max((kv_end - 1) >> a.log2_block, 0);
   const int64_t head_off = static_cast<int64_t>(head) * a.c_hs;
   const int c_ts = static_cast<int>(a.c_ts);
+  const int c_bs32 = static_cast<int>(a.c_bs);      // used when A32
+  const int head_off32 = static_cast<int>(head_off);  // used when A32
   // This wave's rows all lie in one 16-key half of the tile.
   const bool wave_half = wave * kRowsPerWave >= 16;
   int ld_key[kRowsPerWave / 4], ld_k[kRowsPerWave / 4], ld_v[kRowsPerWave / 4];
@@ -235,12 +241,22 @@ __global__ __launch_bounds__(kThreads, 3) void paged_prefill_mfma_kernel(const A
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         ok[h] = ids[h] >= 0 && ids[h] < a.num_blocks;
-        base[h] = static_cast<int64_t>(ok[h] ? ids[h] : 0) * a.c_bs +
-                  ((t0 + h * 16) & (a.block_size - 1)) * a.c_ts + head_off;
+        const int row = (t0 + h * 16) & (a.block_size - 1);
+        if constexpr (A32) {
+          base[h] = (ok[h] ? ids[h] : 0) * c_bs32 + row * c_ts + head_off32;
+        } else {
+          base[h] = static_cast<int64_t>(ok[h] ? ids[h] : 0) * a.c_bs + row * a.c_ts + head_off;
+        }
       }
     } else {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) base[h] = (krow0 + t0 + h * 16) * a.c_ts + head_off;
+      for (int h = 0; h < 2; ++h) {
+        if constexpr (A32) {
+          base[h] = (static_cast<int>(krow0) + t0 + h * 16) * c_ts + head_off32;
+        } else {
+          base[h] = (krow0 + t0 + h * 16) * a.c_ts + head_off;
+        }
+      }
     }
     const int64_t wbase = wave_half ? base[1] : base[0];
     const bool wok = wave_half ? ok[1] : ok[0];
@@ -438,12 +454,28 @@ __global__ __launch_bounds__(kThreads, 3) void paged_prefill_mfma_kernel(const A
     }
 }
 
+// Largest element offset a tile base computation can form, for the A32
+// choice: the last row of the last block (paged) or up to a tile past the
+// last row (contiguous: bases of a tile's rows past the end are formed, then
+// replaced by the safe row), plus the other heads and a head row.
+int64_t max_cache_offset(const AttnArgs& a) {
+  const int64_t rows = a.tables != nullptr
+                           ? static_cast<int64_t>(a.num_blocks - 1) * a.c_bs +
+                                 static_cast<int64_t>(a.block_size - 1) * a.c_ts
+                           : static_cast<int64_t>(a.num_blocks + kKeys) * a.c_ts;
+  return rows + static_cast<int64_t>(a.num_kv_heads - 1) * a.c_hs + a.head_dim;
+}
+
 template <typename E, int G>
 int32_t launch_g(const AttnArgs& a, hipStream_t stream) {
   constexpr int BM = kRows * kWaves / G;
   const int64_t blocks = (static_cast<int64_t>(a.num_rows) + BM - 1) / BM + a.num_seqs;
   const dim3 grid(static_cast<uint32_t>(blocks * a.num_kv_heads));
-  paged_prefill_mfma_kernel<E, G><<<grid, kThreads, 0, stream>>>(a);
+  const bool a32 = a.c_bs >= 0 && a.c_hs >= 0 && max_cache_offset(a) < (int64_t(1) << 31);
+  if (a32)
+    paged_prefill_mfma_kernel<E, G, true><<<grid, kThreads, 0, stream>>>(a);
+  else
+    paged_prefill_mfma_kernel<E, G, false><<<grid, kThreads, 0, stream>>>(a);
   return check_launch("paged prefill (MFMA)");
 }
 

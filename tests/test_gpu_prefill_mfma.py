@@ -7,7 +7,8 @@ decode/prefill tolerance for 16-bit inputs. The cases cover query blocks that
 end inside a 32-row MFMA tile, 32-key tiles that end inside a cache block,
 prefixes shorter and longer than a tile, single-row (decode) requests in the
 same launch, every block size the kernel takes, invalid table entries and
-poison in unused slots, and contiguous K/V.
+poison in unused slots, contiguous K/V, and pools past 2^31 elements
+(64-bit tile addressing) against the same blocks in a small pool.
 """
 
 import math
@@ -163,3 +164,27 @@ def test_long_prefix_chunk():
     out = _run(q, kc, vc, tables, cu_q, cu_k)
     expected = oracle_prefill(q, kc, vc, tables, contexts, cu_q, 1 / math.sqrt(D))
     assert max_abs(out, expected) <= 2e-2
+
+
+def test_pool_beyond_int32_offsets_matches_small_pool():
+    # A pool of more than 2^31 elements per cache (> 4 GiB each in bf16) takes
+    # the 64-bit tile addressing; blocks near its top must give exactly what
+    # the same blocks give in a small pool (32-bit addressing) and match the
+    # oracle.
+    hkv, bs = 8, 16
+    big_blocks = (1 << 31) // (bs * hkv * D) + 64
+    q_lens, prefixes = [40, 1, 96], [100, 700, 33]
+    q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, 32, hkv, bs,
+                                                          torch.bfloat16, 7)
+    top = big_blocks - kc.shape[0]  # small block b lives at big block top + b
+    big_k = torch.empty(big_blocks, bs, hkv, D, dtype=torch.bfloat16, device=DEV)
+    big_v = torch.empty_like(big_k)
+    big_k[top:] = kc
+    big_v[top:] = vc
+    big_tables = torch.where(tables >= 0, tables + top, tables)
+    small = _run(q, kc, vc, tables, cu_q, cu_k)
+    big = _run(q, big_k, big_v, big_tables, cu_q, cu_k)
+    del big_k, big_v
+    assert torch.equal(small, big)
+    expected = oracle_prefill(q, kc, vc, tables, contexts, cu_q, 1 / math.sqrt(D))
+    assert max_abs(big, expected) <= 2e-2
