@@ -231,34 +231,43 @@ __global__ __launch_bounds__(kThreads, 3) void paged_prefill_mfma_kernel(const A
   // (bit h: its 16-key half h has a valid block id).
   auto issue_tile = [&](int tile, R* kbuf, R* vbuf) {
     const int t0 = tile * kKeys;
-    int64_t base[2];
+    const int wt0 = t0 + (wave_half ? 16 : 0);  // first key of this wave's half
+    int64_t wbase;
     bool ok[2] = {true, true};
     if (paged) {
+      // Both halves' block ids (one 8-byte scalar load when they are adjacent
+      // table entries, both at most last_blk), then this wave's half's base.
       const ConstI32* ctab = (const ConstI32*)(trow);
-      const int id0 = ctab[min(t0 >> a.log2_block, last_blk)];
-      const int id1 = ctab[min((t0 + 16) >> a.log2_block, last_blk)];
-      const int ids[2] = {id0, id1};
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        ok[h] = ids[h] >= 0 && ids[h] < a.num_blocks;
-        const int row = (t0 + h * 16) & (a.block_size - 1);
-        if constexpr (A32) {
-          base[h] = (ok[h] ? ids[h] : 0) * c_bs32 + row * c_ts + head_off32;
-        } else {
-          base[h] = static_cast<int64_t>(ok[h] ? ids[h] : 0) * a.c_bs + row * a.c_ts + head_off;
-        }
+      const int e0 = min(t0 >> a.log2_block, last_blk);
+      const int e1 = min((t0 + 16) >> a.log2_block, last_blk);
+      int id0, id1;
+      if (e1 == e0 + 1) {
+        typedef int32_t int2v __attribute__((ext_vector_type(2)));
+        using ConstI32x2 = __attribute__((address_space(4))) const int2v;
+        const int2v both = *(const ConstI32x2*)(ctab + e0);
+        id0 = both.x;
+        id1 = both.y;
+      } else {
+        id0 = ctab[e0];
+        id1 = e1 == e0 ? id0 : ctab[e1];
+      }
+      ok[0] = id0 >= 0 && id0 < a.num_blocks;
+      ok[1] = id1 >= 0 && id1 < a.num_blocks;
+      const int wid = wave_half ? id1 : id0;
+      const bool wk = wave_half ? ok[1] : ok[0];
+      const int row = wt0 & (a.block_size - 1);
+      if constexpr (A32) {
+        wbase = (wk ? wid : 0) * c_bs32 + row * c_ts + head_off32;
+      } else {
+        wbase = static_cast<int64_t>(wk ? wid : 0) * a.c_bs + row * a.c_ts + head_off;
       }
     } else {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if constexpr (A32) {
-          base[h] = (static_cast<int>(krow0) + t0 + h * 16) * c_ts + head_off32;
-        } else {
-          base[h] = (krow0 + t0 + h * 16) * a.c_ts + head_off;
-        }
+      if constexpr (A32) {
+        wbase = (static_cast<int>(krow0) + wt0) * c_ts + head_off32;
+      } else {
+        wbase = (krow0 + wt0) * a.c_ts + head_off;
       }
     }
-    const int64_t wbase = wave_half ? base[1] : base[0];
     const bool wok = wave_half ? ok[1] : ok[0];
 #pragma unroll
     for (int i = 0; i < kRowsPerWave / 4; ++i) {
