@@ -519,8 +519,9 @@ def main() -> int:
                              "known-size kernel that scales FETCH_SIZE / WRITE_SIZE)")
     args = parser.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the decode shards by request or KV head with no exchange; see DESIGN.md).",
+        print("bench.py measures one GPU only: there is no multi-GPU path (paged "
+              "attention shards by request or by KV head with no exchange between GPUs, "
+              "so each GPU runs this same single-GPU launch on its share).",
               file=sys.stderr)
         return 2
 

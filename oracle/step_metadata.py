@@ -1,7 +1,7 @@
 """numpy restatement of MicroInfer's per-step metadata build (test infrastructure).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
-leg may import this module. It is the checker, never the thing measured or
+leg may import this module. It is what results are compared with, never the thing measured or
 shipped.
 
 A scheduled sequence is any object with ``len()``, indexing over its token
