@@ -495,6 +495,155 @@ def step_metadata_cpu_baseline(torch, steps, builder, batch, width, num_blocks, 
     }
 
 
+def _qk_norm_rope_inputs(torch, dev, tokens, hq, hkv, d, num_blocks, block_size, seed):
+    from microinfer_amd.layer.hip_qk_norm_rope import rope_tables
+
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    qkv = torch.randn((tokens, (hq + 2 * hkv) * d), generator=gen, device=dev).to(torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(d, generator=gen, device=dev)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(d, generator=gen, device=dev)).to(torch.bfloat16)
+    cos, sin = rope_tables(40960, d, 1_000_000.0, device=dev)
+    rng = np.random.default_rng(seed)
+    positions = torch.tensor(rng.integers(0, 40960, tokens), dtype=torch.int64, device=dev)
+    slots = torch.tensor(rng.permutation(num_blocks * block_size)[:tokens], dtype=torch.int32,
+                         device=dev)
+    return qkv, qw, kw, cos, sin, positions, slots
+
+
+def run_qk_norm_rope(args) -> int:
+    """Fused Q/K RMSNorm + RoPE + KV append for the 4120 tokens of the mixed
+    chunked-prefill step (Qwen3-8B heads: 32 Q / 8 KV, head_dim 128, bf16,
+    pool 65536 blocks of 16), one launch per step; the 0.6B decode step (32
+    tokens, 16 / 8 heads) is timed beside it (launch-bound)."""
+    import torch
+
+    from microinfer_amd.layer.hip_qk_norm_rope import qk_norm_rope_append
+
+    dev = torch.device("cuda", 0)
+    tokens, hq, hkv, d, num_blocks, block_size = 4120, 32, 8, 128, 65536, 16
+    kc = torch.zeros((num_blocks, block_size, hkv, d), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    qkv, qw, kw, cos, sin, positions, slots = _qk_norm_rope_inputs(
+        torch, dev, tokens, hq, hkv, d, num_blocks, block_size, 0)
+
+    def step(x, n_q, n_kv, pos, slot):
+        return qk_norm_rope_append(x, q_weight=qw, k_weight=kw, eps=1e-6, cos_table=cos,
+                                   sin_table=sin, positions=pos, num_q_heads=n_q,
+                                   num_kv_heads=n_kv, head_dim=d, slot_mapping=slot,
+                                   key_cache=kc[:, :, :n_kv], value_cache=vc[:, :, :n_kv])
+
+    def timed(fn, k):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(k):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / k * 1e3
+
+    run = lambda: step(qkv, hq, hkv, positions, slots)  # noqa: E731
+    warm_up(torch, run, args)
+    us = timed(run, args.steps)
+    # Algorithmic bytes: the fused rows read, Q written, K and V cache rows
+    # written, the cos/sin rows gathered, positions and slots read.
+    es = 2
+    nbytes = (tokens * (hq + 2 * hkv) * d * es + tokens * hq * d * es
+              + tokens * 2 * hkv * d * es + tokens * d * 4 + tokens * 12)
+    achieved = nbytes / (us * 1e-6) / 1e9
+    # The 0.6B decode step: 28 layer launches of 32 tokens, replayed from a
+    # hipGraph so the time is the launches', not the Python wrapper's.
+    small = _qk_norm_rope_inputs(torch, dev, 32, 16, 8, d, num_blocks, block_size, 1)
+    dec = lambda: step(small[0], 16, 8, small[5], small[6])  # noqa: E731
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        dec()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(28):
+            dec()
+    for _ in range(args.warmup):
+        graph.replay()
+    dec_us = timed(graph.replay, args.steps) / 28
+    log(f"{us:.2f} us per 4120-token launch ({achieved:.0f} GB/s), "
+        f"{dec_us:.2f} us per 32-token decode launch")
+    result = {
+        "metric": "fused QK RMSNorm + RoPE + KV append HBM GB/s (% peak)",
+        "value": round(achieved, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "warmup_seconds": args.warmup_seconds,
+        "ms_per_step": round(us / 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) fused QKV rows, random positions < 40960, "
+                "distinct random slots",
+        "config": {
+            "workload": ("Q/K RMSNorm + RoPE (split-half, base 1e6) + KV append of the 4120 "
+                         "tokens of the mixed chunked-prefill step, Qwen3-8B heads (32 Q / "
+                         "8 KV, head_dim 128), bf16, pool 65536 blocks of 16, one launch"),
+            "tokens": tokens,
+            "decode_launch_us": round(dec_us, 3),
+            "decode_launch": ("Qwen3-0.6B heads (16 Q / 8 KV), 32 tokens: 28 launches "
+                              "replayed from a hipGraph, time per launch (launch-bound)"),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "qk_norm_rope_kernel",
+            "bytes_per_launch": nbytes,
+            "us_per_launch": round(us, 3),
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = qk_norm_rope_cpu_baseline(torch, qkv, qw, kw, cos, sin,
+                                                           positions, slots, hq, hkv, d)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def qk_norm_rope_cpu_baseline(torch, qkv, qw, kw, cos, sin, positions, slots, hq, hkv, d,
+                              sample: int = 1024, runs: int = 5):
+    """The oracle's restatement on the host over the first ``sample`` tokens."""
+    from oracle import qk_norm_rope as ref
+
+    x = qkv[:sample].float().cpu().numpy()
+    w_q, w_k = qw.float().cpu().numpy(), kw.float().cpu().numpy()
+    c, s_ = cos.cpu().numpy(), sin.cpu().numpy()
+    pos = positions[:sample].cpu().numpy()
+    slot = slots[:sample].cpu().numpy() % (64 * 16)
+    kc = np.zeros((64, 16, hkv, d), dtype=np.float32)
+    vc = np.zeros_like(kc)
+    times = []
+    for i in range(runs + 1):
+        t0 = time.perf_counter()
+        ref.qk_norm_rope_append(x, w_q, w_k, 1e-6, c, s_, pos, slot, kc, vc, num_q_heads=hq,
+                                num_kv_heads=hkv, head_dim=d, interleaved=False, dtype="bf16")
+        if i:
+            times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    nbytes = (sample * (hq + 2 * hkv) * d * 2 + sample * hq * d * 2 + sample * 2 * hkv * d * 2
+              + sample * d * 4 + sample * 12)
+    return {
+        "value": round(nbytes / sec / 1e9, 3),
+        "unit": "GB/s",
+        "cores": blas_threads(),
+        "kind": "port",
+        "sample": f"{sample} of the 4120 tokens (same bytes formula), x {runs} runs after 1 "
+                  f"warm-up, median {sec * 1e3:.1f} ms; numpy on the host CPU ({cpu_model()})",
+    }
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -506,10 +655,11 @@ def main() -> int:
     parser.add_argument("--layout", default="head_major", choices=["head_major", "token_major"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--workload", default="decode",
-                        choices=["decode", "prefill", "step-metadata"],
+                        choices=["decode", "prefill", "step-metadata", "qk-norm-rope"],
                         help="decode: the headline paged-decode line; prefill: the mixed "
                              "chunked-prefill (MFMA) line; step-metadata: the decode step's "
-                             "device-built metadata")
+                             "device-built metadata; qk-norm-rope: the fused Q/K RMSNorm + "
+                             "RoPE + KV append")
     parser.add_argument("--no-graph", action="store_true",
                         help="decode: launch the step eagerly (for per-dispatch counter runs)")
     parser.add_argument("--graph", action="store_true",
@@ -530,6 +680,8 @@ def main() -> int:
         return run_prefill(args)
     if args.workload == "step-metadata":
         return run_step_metadata(args)
+    if args.workload == "qk-norm-rope":
+        return run_qk_norm_rope(args)
 
     import torch
 

@@ -279,6 +279,48 @@ int32_t mi_step_metadata(const int32_t* cu_seqlens_q, const int32_t* starts,
                          int32_t* slot_mapping, int64_t* positions, int64_t* input_ids,
                          void* stream);
 
+/*
+ * Fused Q/K RMSNorm + RoPE + KV append of one layer's step, from the fused
+ * QKV projection rows qkv[t] = [q heads | k heads | v heads] (each head_dim
+ * elements, row t at qkv + t * qkv_token_stride):
+ *   q_out[t, h] = rope(rms_norm(q[t, h], q_weight), positions[t])
+ *   k'[t, h]    = rope(rms_norm(k[t, h], k_weight), positions[t])
+ *   cache K[slot_mapping[t], h] = k'[t, h], cache V[slot_mapping[t], h] = v[t, h]
+ * rms_norm(x, w) = x * (1 / sqrt(mean(x^2) + eps)) * w in float32, rounded to
+ * dtype; rope rotates the pairs (i, i + D/2) (interleaved = 0, Qwen) or
+ * (2i, 2i + 1) (interleaved = 1) by cos/sin_table[positions[t], i] (float32
+ * tables [table_len, D/2], as RotaryCache builds them) in float32 and rounds
+ * to dtype.
+ *
+ * Replaces Attention.forward's q_norm / k_norm / rotary.apply on Q and K
+ * (microinfer/layer/transformer.py:186-233 with norm.py:26-35 and
+ * rope.py:6-20, :74-85; the prefill-only compiled form
+ * _compiled_qk_norm_rope, transformer.py:18-30) and the append that
+ * CachedAttention.forward does before attending (cached_attention.py:76-85,
+ * worker/kv_cache.py:52-79), in one launch.
+ * slot_mapping may be NULL (no append; the caches are not touched); slot -1
+ * skips a token's append. k_out (optional, may be NULL) receives k' for
+ * callers that also attend to the new rows directly. positions are int32 or
+ * int64 (positions_int64); a position outside [0, table_len) yields zero rows
+ * in q_out / k_out and no append. head_dim is a power of two from two 16-byte
+ * vectors (16 elements for bf16/f16, 8 for fp32) to 256; qkv, q_out, k_out,
+ * the caches and the weights are 16-byte aligned, and every row and head
+ * stride is a whole number of 16-byte vectors.
+ */
+int32_t mi_qk_norm_rope_append(const void* qkv, int64_t qkv_token_stride, const void* q_weight,
+                               const void* k_weight, float eps, const float* cos_table,
+                               const float* sin_table, int32_t table_len,
+                               const void* positions, int32_t positions_int64,
+                               const int32_t* slot_mapping, void* q_out,
+                               int64_t q_out_token_stride, int64_t q_out_head_stride,
+                               void* k_out, int64_t k_out_token_stride,
+                               int64_t k_out_head_stride, void* key_cache, void* value_cache,
+                               int64_t cache_block_stride, int64_t cache_token_stride,
+                               int64_t cache_head_stride, int32_t num_tokens,
+                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                               int32_t interleaved, int32_t block_size, int32_t num_blocks,
+                               int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

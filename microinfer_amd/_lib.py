@@ -47,6 +47,11 @@ SIGNATURES = {
          _P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P, _P, _I64, _I64,
          _P, _I64, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P],
     ),
+    "mi_qk_norm_rope_append": (
+        _I32,
+        [_P, _I64, _P, _P, _F32, _P, _P, _I32, _P, _I32, _P, _P, _I64, _I64, _P, _I64, _I64,
+         _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P],
+    ),
     "mi_decode_plan_bytes": (_I64, [_I32, _I32, _I32]),
     "mi_decode_plan": (_I32, [_P, _I32, _I32, _I32, _I32, _I32, _P, _I64, _P]),
     "mi_paged_prefill": (
