@@ -644,6 +644,122 @@ def qk_norm_rope_cpu_baseline(torch, qkv, qw, kw, cos, sin, positions, slots, hq
     }
 
 
+def run_greedy(args) -> int:
+    """Greedy selection over the logits of the 0.6B decode step: 32 rows of
+    the Qwen3 vocabulary (151936), bf16, one launch (the argmax the decode
+    graph captures). torch.argmax on the same rows is timed beside it."""
+    import torch
+
+    from microinfer_amd.layer.hip_sampler import greedy_argmax
+
+    dev = torch.device("cuda", 0)
+    rows, vocab = 32, 151936
+    gen = torch.Generator(device=dev).manual_seed(0)
+    logits = torch.randn((rows, vocab), generator=gen, device=dev).to(torch.bfloat16)
+    out = torch.empty(rows, dtype=torch.int64, device=dev)
+
+    def timed(fn, k):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(k):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / k * 1e3
+
+    run = lambda: greedy_argmax(logits, out=out)  # noqa: E731
+    warm_up(torch, run, args)
+    eager_us = timed(run, args.steps)
+    # The decode graph replays the launch with no host work around it: time
+    # 20 back-to-back launches captured in a hipGraph (after one call on the
+    # capture stream, which creates that stream's zeroed row state).
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for _ in range(20):
+            run()
+    for _ in range(args.warmup):
+        graph.replay()
+    us = timed(graph.replay, args.steps) / 20
+    ref = lambda: torch.argmax(logits, dim=-1)  # noqa: E731
+    for _ in range(args.warmup):
+        ref()
+    torch_us = timed(ref, args.steps)
+    assert torch.equal(out, torch.argmax(logits, dim=-1))
+    nbytes = rows * vocab * 2 + rows * 8  # logits read, tokens written
+    achieved = nbytes / (us * 1e-6) / 1e9
+    log(f"{us:.2f} us per launch in a graph ({achieved:.0f} GB/s), {eager_us:.2f} us per eager "
+        f"call; torch.argmax {torch_us:.2f} us")
+    result = {
+        "metric": "greedy argmax over decode logits HBM GB/s (% peak)",
+        "value": round(achieved, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "warmup_seconds": args.warmup_seconds,
+        "ms_per_step": round(us / 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) logits",
+        "config": {
+            "workload": ("greedy token selection (argmax, first index of the maximum) over "
+                         "32 rows x 151936 bf16 logits, the 0.6B decode step's batch, one "
+                         "launch"),
+            "rows": rows,
+            "vocab": vocab,
+            "timing": "20 launches replayed from a hipGraph, time per launch",
+            "eager_call_us": round(eager_us, 3),
+            "torch_argmax_us": round(torch_us, 3),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "greedy_argmax_kernel",
+            "bytes_per_launch": nbytes,
+            "us_per_launch": round(us, 3),
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = greedy_cpu_baseline(logits, nbytes)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def greedy_cpu_baseline(logits, nbytes, runs: int = 5):
+    """The oracle's restatement on the host over all 32 rows."""
+    from oracle.greedy import greedy_argmax as ref
+
+    host = logits.float().cpu().numpy()
+    times = []
+    for i in range(runs + 1):
+        t0 = time.perf_counter()
+        ref(host)
+        if i:
+            times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    return {
+        "value": round(nbytes / sec / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"all 32 rows (same bytes formula, bf16 logits widened once before timing), "
+                  f"x {runs} runs after 1 warm-up, median {sec * 1e3:.1f} ms; numpy on the "
+                  f"host CPU ({cpu_model()})",
+    }
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -655,11 +771,12 @@ def main() -> int:
     parser.add_argument("--layout", default="head_major", choices=["head_major", "token_major"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--workload", default="decode",
-                        choices=["decode", "prefill", "step-metadata", "qk-norm-rope"],
+                        choices=["decode", "prefill", "step-metadata", "qk-norm-rope",
+                                 "greedy"],
                         help="decode: the headline paged-decode line; prefill: the mixed "
                              "chunked-prefill (MFMA) line; step-metadata: the decode step's "
                              "device-built metadata; qk-norm-rope: the fused Q/K RMSNorm + "
-                             "RoPE + KV append")
+                             "RoPE + KV append; greedy: the argmax over decode logits")
     parser.add_argument("--no-graph", action="store_true",
                         help="decode: launch the step eagerly (for per-dispatch counter runs)")
     parser.add_argument("--graph", action="store_true",
@@ -682,6 +799,8 @@ def main() -> int:
         return run_step_metadata(args)
     if args.workload == "qk-norm-rope":
         return run_qk_norm_rope(args)
+    if args.workload == "greedy":
+        return run_greedy(args)
 
     import torch
 

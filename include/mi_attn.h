@@ -321,6 +321,23 @@ int32_t mi_qk_norm_rope_append(const void* qkv, int64_t qkv_token_stride, const 
                                int32_t interleaved, int32_t block_size, int32_t num_blocks,
                                int32_t dtype, void* stream);
 
+/*
+ * Greedy token selection: tokens[r] = argmax over v of logits[r * row_stride
+ * + v], v in [0, vocab_size), as int64 -- the `logits.argmax(-1)` that
+ * ModelRunner captures into each decode graph (microinfer/runner.py:236-240)
+ * and calls for greedy rows (runner.py:618-625, layer/sampler.py:44-45).
+ * torch's order: NaN above every number, the first index among equal maxima,
+ * -0 equal to +0. vocab_size is at most 2^30.
+ * `state` is per-stream scratch of mi_greedy_argmax_state_bytes(num_rows)
+ * bytes, 8-byte aligned, zero-filled once by the caller; every launch leaves
+ * it zero again. Launches that may run concurrently need separate state.
+ * Capture-safe (one launch, no allocation, no memset).
+ */
+int64_t mi_greedy_argmax_state_bytes(int32_t num_rows);
+int32_t mi_greedy_argmax(const void* logits, int64_t row_stride, int32_t num_rows,
+                         int32_t vocab_size, int32_t dtype, int64_t* tokens, void* state,
+                         int64_t state_bytes, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

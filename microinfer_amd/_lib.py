@@ -64,6 +64,8 @@ SIGNATURES = {
         [_P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P, _I32, _I32, _P, _P, _I32, _I32,
          _I32, _I32, _I32, _P],
     ),
+    "mi_greedy_argmax_state_bytes": (_I64, [_I32]),
+    "mi_greedy_argmax": (_I32, [_P, _I64, _I32, _I32, _I32, _P, _P, _I64, _P]),
     "mi_step_metadata": (
         _I32,
         [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _I64, _I32, _P, _P, _P, _P,

@@ -29,6 +29,7 @@ import numpy as np
 import torch
 
 from microinfer_amd import _lib
+from microinfer_amd.layer.hip_sampler import greedy_argmax
 from microinfer_amd.layer.metadata import AttentionMetadata
 
 _INT32_MAX = 2 ** 31 - 1
@@ -334,17 +335,21 @@ class DecodeGraphRunner:
 
     ``forward(input_ids, positions, metadata)`` is the step to capture (the
     model's decode forward, or here the attention layers); it must be
-    capture-safe.
+    capture-safe. With ``greedy`` its output is ``[batch, vocab]`` logits and
+    the graph also selects each row's greedy token with the HIP argmax
+    (runner.py:236-240); ``run`` then returns ``(logits, tokens)`` like
+    ``_run_decode`` (runner.py:603).
     """
 
     def __init__(self, builder: StepMetadataBuilder, forward, *, max_num_seqs: int,
-                 table_width: int):
+                 table_width: int, greedy: bool = False):
         if builder.pad_block_id is None:
             raise ValueError("graph buckets need the builder's pad block")
         if builder.device.type != "cuda":
             raise RuntimeError("graph capture needs a HIP device")
         self.builder = builder
         self.forward = forward
+        self.greedy = greedy
         self.table_width = table_width
         self.buckets = []
         self.pool = None
@@ -360,19 +365,24 @@ class DecodeGraphRunner:
         side.wait_stream(torch.cuda.current_stream(device))
         with torch.cuda.stream(side), torch.inference_mode():
             for _ in range(2):
-                self.forward(ids, positions, buffers.metadata(batch))
+                self._step(ids, positions, buffers.metadata(batch))
         torch.cuda.current_stream(device).wait_stream(side)
         torch.cuda.synchronize(device)
         graph = torch.cuda.CUDAGraph()
         # Captured on the warm-up stream, so per-stream state the library
-        # created during the warm-up (the decode arrival counters) is reused
-        # rather than allocated and zero-filled inside the graph.
+        # created during the warm-up (the decode arrival counters, the argmax
+        # row slots) is reused rather than allocated and zero-filled inside
+        # the graph.
         with torch.cuda.graph(graph, self.pool, stream=side), torch.inference_mode():
-            out = self.forward(ids, positions, buffers.metadata(batch))
+            out = self._step(ids, positions, buffers.metadata(batch))
         if self.pool is None:
             self.pool = graph.pool()
         torch.cuda.synchronize(device)
         self.buckets.append((batch, buffers, graph, out))
+
+    def _step(self, ids, positions, metadata):
+        out = self.forward(ids, positions, metadata)
+        return (out, greedy_argmax(out)) if self.greedy else out
 
     def select(self, batch: int):
         for bucket in self.buckets:
@@ -389,4 +399,7 @@ class DecodeGraphRunner:
         batch, buffers, graph, out = bucket
         self.builder.fill_decode(buffers, seqs, rows=batch)
         graph.replay()
-        return out[:len(seqs)]
+        n = len(seqs)
+        if self.greedy:
+            return out[0][:n], out[1][:n]
+        return out[:n]
