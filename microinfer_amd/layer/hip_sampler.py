@@ -68,3 +68,45 @@ def greedy_argmax(logits: torch.Tensor, *, out: torch.Tensor | None = None) -> t
         out.data_ptr(), state.data_ptr(), state.numel() * 8, stream)
     _lib.check(status, "mi_greedy_argmax")
     return out
+
+
+class Sampler:
+    """Temperature sampling with the device argmax.
+
+    Mirrors ``Sampler`` (microinfer/layer/sampler.py:5-50): probabilities
+    are a softmax of the row-centred logits over the temperature; a sample is
+    ``argmax(probabilities / noise)`` with exponential noise (the
+    Gumbel-max construction), taken with ``greedy_argmax``; ``greedy=True``
+    returns the argmax of the logits. ``validate`` checks the same contract.
+    """
+
+    def __init__(self, validate: bool = True):
+        self.validate = validate
+
+    def _validate(self, logits, temperatures):
+        if logits.ndim != 2 or logits.shape[1] == 0 or not logits.dtype.is_floating_point:
+            raise ValueError("logits must be floating [requests, vocabulary]")
+        if temperatures.shape != (logits.shape[0],) or temperatures.device != logits.device:
+            raise ValueError("temperature shape/device does not match logits")
+        if not torch.isfinite(temperatures).all() or (temperatures <= 0).any():
+            raise ValueError("temperatures must be finite and positive")
+        if (torch.isnan(logits).any() or torch.isposinf(logits).any()
+                or not torch.isfinite(logits).any(-1).all()):
+            raise ValueError("each logits row must contain finite values, without NaN/+inf")
+
+    def probabilities(self, logits, temperatures):
+        if self.validate:
+            self._validate(logits, temperatures)
+        work = logits.float()
+        work = (work - work.amax(-1, keepdim=True)) / temperatures[:, None]
+        return work.softmax(-1)
+
+    def sample(self, logits, temperatures, *, generator=None, greedy=False):
+        probabilities = self.probabilities(logits, temperatures)
+        if greedy:
+            return greedy_argmax(logits)
+        noise = torch.empty_like(probabilities).exponential_(generator=generator)
+        return greedy_argmax(probabilities / noise)
+
+    def __call__(self, logits, temperatures):
+        return self.sample(logits, temperatures)
