@@ -760,6 +760,150 @@ def greedy_cpu_baseline(logits, nbytes, runs: int = 5):
     }
 
 
+def run_engine(args) -> int:
+    """The engine on random-init Qwen3-0.6B (28 layers, bf16): 64 requests of
+    128 uniform-random prompt ids arriving together, greedy, 16 output tokens
+    each, ignoring EOS; block 16, 4096 blocks, decode from hipGraph buckets,
+    mixed batches, max_num_seqs 64, max_num_batched_tokens 4096,
+    max_num_prefill_tokens 512. A step of the bench is one such batch run to
+    completion (fresh prompts each time)."""
+    import torch
+
+    from microinfer_amd.engine.blockmanager import BlockManager
+    from microinfer_amd.engine.config import EngineConfig, SampleParameter
+    from microinfer_amd.engine.llm_engine import LLMEngine
+    from microinfer_amd.engine.model import QwenConfig, Qwen3Model
+    from microinfer_amd.engine.model_runner import ModelRunner
+    from microinfer_amd.engine.scheduler import Scheduler
+    from microinfer_amd.engine.sequence import Sequence
+
+    requests, prompt_len, out_len = 64, 128, 16
+    config = EngineConfig(max_num_seqs=64, max_num_batched_tokens=4096,
+                          max_num_prefill_tokens=512, max_model_len=4096,
+                          use_cuda_graph=True, mixed_batch=True)
+    model_config = QwenConfig()
+    log("building random-init Qwen3-0.6B and capturing decode graphs")
+    model = Qwen3Model(model_config, dtype=torch.bfloat16, device="cuda", seed=0)
+    runner = ModelRunner(model, config, num_blocks=4096, block_size=16)
+    manager = BlockManager(4096, 16)
+    engine = LLMEngine(Scheduler(config, manager), runner)
+    params = SampleParameter(max_tokens=out_len, ignore_eos=True, greedy=True)
+
+    def one_batch(seed):
+        rng = np.random.default_rng(seed)
+        seqs = [Sequence(rng.integers(0, model_config.vocab_size, prompt_len).tolist(), params)
+                for _ in range(requests)]
+        for seq in seqs:
+            engine.add_request(seq)
+        decode_s, decode_tokens, steps = 0.0, 0, 0
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        while not engine.is_finished():
+            t0 = time.perf_counter()
+            _, num_tokens = engine.step()  # returns host token ids: synchronised
+            if num_tokens < 0:
+                decode_s += time.perf_counter() - t0
+                decode_tokens -= num_tokens
+            steps += 1
+        wall = time.perf_counter() - start
+        assert all(len(s.completion_token_ids) == out_len for s in seqs)
+        return wall, decode_s, decode_tokens, steps
+
+    for i in range(max(1, args.warmup)):
+        one_batch(1000 + i)
+        manager.reset_prefix_cache()
+    walls, decodes, dec_tokens, steps = [], [], 0, 0
+    for i in range(args.steps):
+        wall, dec_s, dec_tok, n = one_batch(i)
+        manager.reset_prefix_cache()
+        walls.append(wall)
+        decodes.append(dec_s)
+        dec_tokens += dec_tok
+        steps += n
+    output_tps = requests * out_len * args.steps / sum(walls)
+    decode_tps = dec_tokens / sum(decodes)
+    decode_step_us = sum(decodes) / (dec_tokens / requests) * 1e6 if dec_tokens else 0.0
+    # A full decode step streams every weight once (28 layers of QKV, output,
+    # gate/up and down projections, the norms and the untied vocabulary
+    # projection) plus the batch's K/V: bytes per step over the step time.
+    c = model_config
+    per_layer = ((c.num_q_head + 2 * c.num_kv_head) * c.head_dim * c.hidden_dim
+                 + c.hidden_dim * c.num_q_head * c.head_dim
+                 + 3 * c.MLP_inter_dim * c.hidden_dim + 2 * c.hidden_dim + 2 * c.head_dim)
+    weight_bytes = 2 * (c.num_hidden_layer * per_layer + c.vocab_size * c.hidden_dim
+                        + c.hidden_dim)
+    mean_ctx = prompt_len + out_len / 2
+    kv_bytes = 2 * 2 * c.num_hidden_layer * requests * mean_ctx * c.num_kv_head * c.head_dim
+    step_bytes = weight_bytes + kv_bytes
+    achieved = step_bytes / (decode_step_us * 1e-6) / 1e9 if decode_step_us else 0.0
+    log(f"{output_tps:.0f} output tok/s over {args.steps} batches "
+        f"({statistics.mean(walls) * 1e3:.1f} ms each), decode {decode_tps:.0f} tok/s, "
+        f"{decode_step_us:.0f} us per decode step")
+    result = {
+        "metric": "engine output tokens/s (random-init Qwen3-0.6B, 64 x 128-token prompts, "
+                  "16 greedy outputs)",
+        "value": round(output_tps, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": max(1, args.warmup),
+        "ms_per_step": round(statistics.mean(walls) * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init weights N(0, 0.02) (seed 0), uniform-random prompt ids",
+        "config": {
+            "workload": ("engine: 64 requests x 128 random prompt ids arriving together, "
+                         "greedy, 16 output tokens (EOS ignored), Qwen3-0.6B random init, "
+                         "block 16, 4096 blocks, hipGraph decode, mixed batches, "
+                         "max_num_seqs 64, max_num_batched_tokens 4096, "
+                         "max_num_prefill_tokens 512; a bench step is one batch to completion"),
+            "decode_tokens_per_s": round(decode_tps, 1),
+            "decode_step_us": round(decode_step_us, 1),
+            "engine_steps_per_batch": steps / args.steps,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "decode step (hipGraph replay: 28 layers of GEMMs, fused Q/K norm + "
+                      "RoPE + append, paged decode; vocabulary projection; argmax), host "
+                      "time included",
+            "bytes_per_launch": int(step_bytes),
+            "us_per_launch": round(decode_step_us, 1),
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = engine_cpu_baseline(model, prompt_len)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def engine_cpu_baseline(model, prompt_len, new_tokens: int = 2):
+    """The dense oracle on the host: one request's 128-token prompt and
+    ``new_tokens`` greedy tokens, each recomputing the whole sequence."""
+    from oracle.qwen3_dense import greedy_generate
+
+    weights = model.host_weights()
+    prompt = np.random.default_rng(99).integers(0, model.config.vocab_size, prompt_len).tolist()
+    t0 = time.perf_counter()
+    greedy_generate(weights, model.config, prompt, new_tokens)
+    sec = time.perf_counter() - t0
+    return {
+        "value": round(new_tokens / sec, 3),
+        "unit": "tokens/s",
+        "cores": blas_threads(),
+        "kind": "port",
+        "sample": f"1 request, {prompt_len}-token prompt, {new_tokens} greedy tokens by the "
+                  f"dense numpy oracle (full recompute per token, float32/float64), "
+                  f"{sec:.1f} s on the host CPU ({cpu_model()})",
+    }
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -772,11 +916,12 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--workload", default="decode",
                         choices=["decode", "prefill", "step-metadata", "qk-norm-rope",
-                                 "greedy"],
+                                 "greedy", "engine"],
                         help="decode: the headline paged-decode line; prefill: the mixed "
                              "chunked-prefill (MFMA) line; step-metadata: the decode step's "
                              "device-built metadata; qk-norm-rope: the fused Q/K RMSNorm + "
-                             "RoPE + KV append; greedy: the argmax over decode logits")
+                             "RoPE + KV append; greedy: the argmax over decode logits; "
+                             "engine: random-init Qwen3-0.6B served by the engine")
     parser.add_argument("--no-graph", action="store_true",
                         help="decode: launch the step eagerly (for per-dispatch counter runs)")
     parser.add_argument("--graph", action="store_true",
@@ -801,6 +946,8 @@ def main() -> int:
         return run_qk_norm_rope(args)
     if args.workload == "greedy":
         return run_greedy(args)
+    if args.workload == "engine":
+        return run_engine(args)
 
     import torch
 
