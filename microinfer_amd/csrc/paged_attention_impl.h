@@ -516,6 +516,27 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
 #endif
 // Waves per workgroup: they split one partition and merge through LDS.
 constexpr int kWavesPerGroup = MI_WAVES_PER_GROUP;
+// Decode launches with more (sequence, KV head) pairs than the device has
+// CUs use half-width workgroups: at about 145 VGPRs a CU holds one 8-wave
+// workgroup but three 4-wave ones, so such a grid runs in one round instead
+// of two. (Qwen3-0.6B heads, 64 sequences of 140 tokens: 12.4 us per launch
+// instead of 15.6; 32 sequences, one 8-wave group per CU, stays faster.)
+constexpr int kNarrowWavesPerGroup = 4;
+
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
 
 constexpr int tile_unroll(int gmax) {
   return gmax <= 2 ? MI_TILE_UNROLL_SMALL_GROUP : MI_TILE_UNROLL_LARGE_GROUP;
@@ -529,18 +550,22 @@ int32_t launch_vector_typed(const AttnArgs& a, hipStream_t stream) {
   const int D = a.head_dim;
   const int G = a.group;
   const dim3 grid((a.varlen ? a.num_rows : a.max_items) * a.num_kv_heads);
+  const bool narrow =
+      !a.varlen && static_cast<int64_t>(a.num_seqs) * a.num_kv_heads > device_cus();
   bool launched = false;
 
+#define MI_VEC_KERNEL(DIM, GM, EX, FAST_, NW_)                                          \
+  paged_attention_vector_kernel<E, ((DIM) < kPackElems ? (DIM) : kPackElems),             \
+                                (DIM) / ((DIM) < kPackElems ? (DIM) : kPackElems), GM, EX, \
+                                tile_unroll(GM), FAST_, NW_><<<grid, kWave * (NW_), 0, stream>>>(a)
 #define MI_VEC_LAUNCH(DIM, GM, EX)                                                     \
   do {                                                                                  \
-    constexpr int VEC_ = (DIM) < kPackElems ? (DIM) : kPackElems;                       \
-    constexpr int LPR_ = (DIM) / VEC_;                                                  \
-    if (a.tables != nullptr && kWave / LPR_ <= a.block_size)                            \
-      paged_attention_vector_kernel<E, VEC_, LPR_, GM, EX, tile_unroll(GM), true,         \
-                                    kWavesPerGroup><<<grid, kWave * kWavesPerGroup, 0, stream>>>(a); \
-    else                                                                                \
-      paged_attention_vector_kernel<E, VEC_, LPR_, GM, EX, tile_unroll(GM), false,        \
-                                    kWavesPerGroup><<<grid, kWave * kWavesPerGroup, 0, stream>>>(a); \
+    constexpr int LPR_ = (DIM) / ((DIM) < kPackElems ? (DIM) : kPackElems);             \
+    const bool fast_ = a.tables != nullptr && kWave / LPR_ <= a.block_size;             \
+    if (fast_ && narrow) MI_VEC_KERNEL(DIM, GM, EX, true, kNarrowWavesPerGroup);         \
+    else if (fast_) MI_VEC_KERNEL(DIM, GM, EX, true, kWavesPerGroup);                    \
+    else if (narrow) MI_VEC_KERNEL(DIM, GM, EX, false, kNarrowWavesPerGroup);            \
+    else MI_VEC_KERNEL(DIM, GM, EX, false, kWavesPerGroup);                              \
     launched = true;                                                                    \
   } while (0)
 
@@ -568,6 +593,7 @@ int32_t launch_vector_typed(const AttnArgs& a, hipStream_t stream) {
   }
 #undef MI_VEC_DIM
 #undef MI_VEC_LAUNCH
+#undef MI_VEC_KERNEL
   if (!launched)
     return fail(MI_ERR_UNSUPPORTED,
                 "paged attention: no kernel for head_dim=" + std::to_string(D) +

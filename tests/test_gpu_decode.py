@@ -287,3 +287,47 @@ def test_hipgraph_replay_tracks_new_contexts():
         torch.cuda.synchronize()
         eager = hip_paged_decode(q, kc, vc, tables, lens)
         assert torch.equal(out, eager), f"replay {step} differs from eager"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (8, 4, 64), (4, 1, 128)])
+def test_many_sequences_take_half_width_groups(dtype, hq, hkv, d):
+    # More (sequence, KV head) pairs than the device has CUs: the launch uses
+    # 4-wave workgroups. Adaptive and forced splits, and the fused append,
+    # must still match the oracle.
+    rng = np.random.default_rng(11)
+    num_seqs, bs = 300 // hkv + 40, 16
+    contexts = rng.integers(1, 400, num_seqs)
+    contexts[3], contexts[7], contexts[-1] = 0, 1, 2500
+    width = int(-(-contexts.max() // bs))
+    pool = int(sum(-(-c // bs) for c in contexts)) + 8
+    perm = rng.permutation(pool)
+    tables = np.full((num_seqs, width), -1, dtype=np.int32)
+    used = 0
+    for r, c in enumerate(contexts):
+        n = int(-(-c // bs))
+        tables[r, :n] = perm[used:used + n]
+        used += n
+    torch.manual_seed(12)
+    kc = torch.randn(pool, bs, hkv, d, device=DEV).to(dtype)
+    vc = torch.randn_like(kc)
+    q = torch.randn(num_seqs, hq, d, device=DEV).to(dtype)
+    t = torch.tensor(tables, device=DEV)
+    lens = torch.tensor(contexts, dtype=torch.int32, device=DEV)
+    expected = oracle_decode(q, kc, vc, t, lens, 1 / math.sqrt(d))
+    assert max_abs(hip_paged_decode(q, kc, vc, t, lens), expected) <= TOLERANCE[dtype]
+    assert max_abs(hip_paged_decode(q, kc, vc, t, lens, split_k=4), expected) <= TOLERANCE[dtype]
+    # Fused append of each sequence's last row == append, then attend.
+    live = contexts > 0
+    new_k = torch.randn(num_seqs, hkv, d, device=DEV).to(dtype)
+    new_v = torch.randn_like(new_k)
+    kc2, vc2 = kc.clone(), vc.clone()
+    fused = hip_paged_decode(q, kc2, vc2, t, lens, new_keys=new_k, new_values=new_v)
+    for r in np.flatnonzero(live):
+        pos = int(contexts[r]) - 1
+        blk = int(tables[r, pos // bs])
+        kc[blk, pos % bs] = new_k[r]
+        vc[blk, pos % bs] = new_v[r]
+    assert torch.equal(kc2, kc) and torch.equal(vc2, vc)
+    expected = oracle_decode(q, kc, vc, t, lens, 1 / math.sqrt(d))
+    assert max_abs(fused, expected) <= TOLERANCE[dtype]
