@@ -904,6 +904,264 @@ def engine_cpu_baseline(model, prompt_len, new_tokens: int = 2):
     }
 
 
+def _graph_time(torch, fn, launches: int, replays: int, warmup: int) -> float:
+    """Microseconds per launch of ``fn`` (which makes ``launches`` launches)
+    replayed from a hipGraph after one call on the capture stream."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        fn()
+    for _ in range(max(1, warmup)):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / replays / launches * 1e3
+
+
+def _hbm_line(metric, achieved, us, nbytes, kernel, args, data, config, cpu=None):
+    result = {
+        "metric": metric,
+        "value": round(achieved, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us / 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": data,
+        "config": config,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": kernel,
+            "bytes_per_launch": int(nbytes),
+            "us_per_launch": round(us, 3),
+        },
+    }
+    if cpu is not None:
+        result["cpu_baseline"] = cpu
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def _median_time(fn, runs: int = 5) -> float:
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def run_append(args) -> int:
+    """KV append of the mixed chunked-prefill step's 4120 tokens (Qwen3-8B KV
+    heads: 8 x 128, bf16) into a 65536-block pool at distinct random slots;
+    20 launches replayed from a hipGraph. The 0.6B decode step's 32-row
+    append is timed beside it (launch-bound)."""
+    import torch
+
+    from microinfer_amd.worker.kv_cache import KVCache
+
+    dev = torch.device("cuda", 0)
+    tokens, hkv, d, num_blocks, bs = 4120, 8, 128, 65536, 16
+    cache = KVCache(1, num_blocks, bs, hkv, d, dtype=torch.bfloat16, device=dev)
+    view = cache.layer(0)
+    rng = np.random.default_rng(0)
+    slots = rng.permutation(num_blocks * bs)[:tokens].astype(np.int32)
+    slot_t = torch.tensor(slots, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    keys = torch.randn((tokens, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
+    values = torch.randn((tokens, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
+    launches = 20
+
+    def many():
+        for _ in range(launches):
+            view.write_slots(slot_t, keys, values)
+
+    us = _graph_time(torch, many, launches, args.steps, args.warmup)
+    small = slot_t[:32].contiguous()
+    small_us = _graph_time(torch, lambda: [view.write_slots(small, keys[:32], values[:32])
+                                           for _ in range(launches)], launches, args.steps,
+                           args.warmup)
+    nbytes = 2 * 2 * tokens * hkv * d * 2 + 4 * tokens  # K and V rows read + written, slots
+    achieved = nbytes / (us * 1e-6) / 1e9
+    log(f"{us:.2f} us per 4120-row append ({achieved:.0f} GB/s), {small_us:.2f} us per 32-row")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import kv_append
+
+        host_k = np.zeros((4096, bs, hkv, d), dtype=np.float32)
+        host_v = np.zeros_like(host_k)
+        k32, v32 = keys.float().cpu().numpy(), values.float().cpu().numpy()
+        host_slots = slots % (4096 * bs)
+        sec = _median_time(lambda: kv_append(host_k, host_v, host_slots, k32, v32))
+        cpu = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1,
+               "kind": "port",
+               "sample": f"all 4120 rows into a 4096-block host pool (same bytes formula), "
+                         f"median of 5 after 1 warm-up, {sec * 1e3:.1f} ms; numpy on the host "
+                         f"CPU ({cpu_model()})"}
+    return _hbm_line(
+        "KV append HBM GB/s (% peak)", achieved, us, nbytes, "kv_append_kernel", args,
+        "synthetic: seeded N(0,1) K/V rows, distinct random slots",
+        {"workload": ("KV append of 4120 tokens (the mixed chunked-prefill step), 8 KV heads x "
+                      "128, bf16, head-major pool of 65536 blocks of 16, distinct random slots; "
+                      "20 launches replayed from a hipGraph, time per launch"),
+         "tokens": tokens, "decode_append_us": round(small_us, 3),
+         "decode_append": "32 rows (the 0.6B decode step), same pool, launch-bound"}, cpu)
+
+
+def run_gather(args) -> int:
+    """Block-table gather of every request of the mixed chunked-prefill step
+    (8 chunks on prefixes U[0,3072] + 24 decode rows, Qwen3-8B KV heads,
+    bf16) into contiguous varlen K/V, one launch."""
+    import torch
+
+    from microinfer_amd.layer.hip_paged_attention import hip_gather_kv
+    from microinfer_amd.workloads import make_mixed_prefill_batch
+
+    dev = torch.device("cuda", 0)
+    batch = make_mixed_prefill_batch()
+    hkv, d, bs = 8, 128, batch.block_size
+    shape = (batch.pool_blocks, bs, hkv, d)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    kc = torch.randn(shape, generator=gen, device=dev).to(torch.bfloat16)
+    vc = torch.randn(shape, generator=gen, device=dev).to(torch.bfloat16)
+    tables = torch.tensor(batch.block_tables, device=dev)
+    contexts = [int(c) for c in batch.context_lens]
+    total = sum(contexts)
+    # The kernel path: cu_seqlens_k already on the device (gather_paged_kv,
+    # the reference-shaped entry, builds it from host contexts each call).
+    cu_k = torch.tensor(batch.cu_seqlens_k, device=dev)
+    run = lambda: hip_gather_kv(kc, vc, tables, cu_k, total)  # noqa: E731
+    warm_up(torch, run, args)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        run()
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) / args.steps * 1e3
+    nbytes = 2 * 2 * total * hkv * d * 2 + 4 * sum(-(-c // bs) for c in contexts)
+    achieved = nbytes / (us * 1e-6) / 1e9
+    log(f"{us:.2f} us per gather of {total} rows ({achieved:.0f} GB/s)")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import gather_paged_kv as ref_gather
+
+        sample = 4
+        used = sorted({int(b) for r in range(sample)
+                       for b in batch.block_tables[r, :-(-contexts[r] // bs)]})
+        remap = {b: i for i, b in enumerate(used)}
+        small = np.full((sample, batch.block_tables.shape[1]), -1, dtype=np.int32)
+        for r in range(sample):
+            for j in range(-(-contexts[r] // bs)):
+                small[r, j] = remap[int(batch.block_tables[r, j])]
+        idx = torch.tensor(used, device=dev)
+        hk = kc.index_select(0, idx).float().cpu().numpy()
+        hv = vc.index_select(0, idx).float().cpu().numpy()
+        sec = _median_time(lambda: ref_gather(hk, hv, small, contexts[:sample], bs))
+        sample_bytes = 2 * 2 * sum(contexts[:sample]) * hkv * d * 2
+        cpu = {"value": round(sample_bytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1,
+               "kind": "port",
+               "sample": f"the first {sample} requests ({sum(contexts[:sample])} rows, same "
+                         f"bytes formula), median of 5 after 1 warm-up, {sec * 1e3:.1f} ms; "
+                         f"numpy on the host CPU ({cpu_model()})"}
+    return _hbm_line(
+        "paged KV gather HBM GB/s (% peak)", achieved, us, nbytes, "gather_kv_kernel", args,
+        "synthetic: seeded N(0,1) pools, mixed-step block tables with shared prefix blocks",
+        {"workload": ("gather of all 32 requests of the mixed chunked-prefill step (8 x 512 "
+                      "chunks on prefixes U[0,3072] + 24 decode rows, U[256,2048]) into "
+                      "contiguous K/V, 8 KV heads x 128, bf16, pool 65536 blocks of 16, one "
+                      "launch"), "rows": total}, cpu)
+
+
+def run_long_decode(args) -> int:
+    """Long-context decode (Qwen3-8B heads: 32 Q / 8 KV, head_dim 128, bf16,
+    pool 65536 blocks of 16): 1 or 4 sequences of 4096 / 16384 / 32768
+    tokens, split into partitions merged in the same launch. Each case
+    replays launches over distinct blocks (more bytes than the last-level
+    cache holds) from a hipGraph; ``value`` is the 4 x 32768 case."""
+    import torch
+
+    from microinfer_amd.layer.hip_paged_attention import decode_plan, hip_paged_decode
+
+    dev = torch.device("cuda", 0)
+    hq, hkv, d, bs, num_blocks = 32, 8, 128, 16, 65536
+    gen = torch.Generator(device=dev).manual_seed(0)
+    kc = torch.randn((num_blocks, bs, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
+    vc = torch.randn((num_blocks, bs, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
+    rng = np.random.default_rng(0)
+    perm = torch.tensor(rng.permutation(num_blocks).astype(np.int32), device=dev)
+    cases = {}
+    for rows in (1, 4):
+        for ctx in (4096, 16384, 32768):
+            nb = ctx // bs
+            launches = min(28, num_blocks // (rows * nb))
+            q = torch.randn((launches, rows, hq, d), generator=gen, device=dev).to(torch.bfloat16)
+            tables = [perm[i * rows * nb:(i + 1) * rows * nb].reshape(rows, nb).contiguous()
+                      for i in range(launches)]
+            lens = torch.full((rows,), ctx, dtype=torch.int32, device=dev)
+
+            def many(q=q, tables=tables, lens=lens, launches=launches, nb=nb):
+                # One partition plan per step, shared by every layer's launch.
+                plan = decode_plan(lens, num_kv_heads=hkv, block_size=bs, block_table_width=nb)
+                for i in range(launches):
+                    hip_paged_decode(q[i], kc, vc, tables[i], lens, plan=plan)
+
+            us = _graph_time(torch, many, launches, max(1, args.steps // 5), args.warmup)
+            nbytes = rows * ctx * hkv * d * 2 * 2 + 2 * rows * hq * d * 2 + rows * nb * 4 + 8 * rows
+            cases[f"{rows}x{ctx}"] = (us, nbytes)
+            log(f"{rows} x {ctx}: {us:.2f} us per launch, {nbytes / us / 1e3:.0f} GB/s")
+    us, nbytes = cases["4x32768"]
+    achieved = nbytes / (us * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import paged_attention_reference
+
+        nb = 4096 // bs
+        idx = perm[:nb].long()
+        hk = kc.index_select(0, idx).float().cpu().numpy()
+        hv = vc.index_select(0, idx).float().cpu().numpy()
+        q1 = torch.randn((1, hq, d), generator=gen, device=dev).to(torch.bfloat16).float()
+        q1 = q1.cpu().numpy()
+        table = np.arange(nb, dtype=np.int32)[None]
+        sec = _median_time(lambda: paged_attention_reference(q1, hk, hv, table, [4096], [0, 1],
+                                                             scale=1 / math.sqrt(d)))
+        sample_bytes = cases["1x4096"][1]
+        cpu = {"value": round(sample_bytes / sec / 1e9, 3), "unit": "GB/s",
+               "cores": blas_threads(), "kind": "port",
+               "sample": f"1 x 4096 (same bytes formula), median of 5 after 1 warm-up, "
+                         f"{sec * 1e3:.1f} ms; numpy/BLAS on the host CPU ({cpu_model()})"}
+    config = {"workload": ("long-context split decode, Qwen3-8B heads (32 Q / 8 KV, head_dim "
+                           "128), bf16, pool 65536 blocks of 16; value: 4 sequences x 32768 "
+                           "tokens, one launch (partitions merged in the launch)"),
+              "cases_us": {k: round(v[0], 2) for k, v in cases.items()},
+              "cases_gbs": {k: round(v[1] / v[0] / 1e3, 1) for k, v in cases.items()},
+              "note": "1 x 4096 (16.8 MB) is launch-latency-bound"}
+    return _hbm_line("long-context paged decode HBM GB/s (% peak)", achieved, us, nbytes,
+                     "paged_attention_vector_kernel (split + in-launch merge)", args,
+                     "synthetic: seeded N(0,1) Q and pools, random distinct block tables",
+                     config, cpu)
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -916,12 +1174,14 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--workload", default="decode",
                         choices=["decode", "prefill", "step-metadata", "qk-norm-rope",
-                                 "greedy", "engine"],
+                                 "greedy", "engine", "append", "gather", "long-decode"],
                         help="decode: the headline paged-decode line; prefill: the mixed "
                              "chunked-prefill (MFMA) line; step-metadata: the decode step's "
                              "device-built metadata; qk-norm-rope: the fused Q/K RMSNorm + "
                              "RoPE + KV append; greedy: the argmax over decode logits; "
-                             "engine: random-init Qwen3-0.6B served by the engine")
+                             "engine: random-init Qwen3-0.6B served by the engine; append, "
+                             "gather, long-decode: the KV append, the block-table gather and "
+                             "long-context split decode")
     parser.add_argument("--no-graph", action="store_true",
                         help="decode: launch the step eagerly (for per-dispatch counter runs)")
     parser.add_argument("--graph", action="store_true",
@@ -948,6 +1208,12 @@ def main() -> int:
         return run_greedy(args)
     if args.workload == "engine":
         return run_engine(args)
+    if args.workload == "append":
+        return run_append(args)
+    if args.workload == "gather":
+        return run_gather(args)
+    if args.workload == "long-decode":
+        return run_long_decode(args)
 
     import torch
 
