@@ -104,6 +104,11 @@ def build_decode_state(torch, layers: int, layout: str):
 PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 DECODE_TRAFFIC = os.path.join(PROFILES, "paged_decode_traffic_qwen3-0.6b_b32.json")
 PREFILL_TRAFFIC = os.path.join(PROFILES, "paged_prefill_traffic_qwen3-8b_mixed.json")
+QK_TRAFFIC = os.path.join(PROFILES, "qk_norm_rope_traffic_qwen3-8b_mixed.json")
+GREEDY_TRAFFIC = os.path.join(PROFILES, "greedy_argmax_traffic_qwen3-vocab_b32.json")
+APPEND_TRAFFIC = os.path.join(PROFILES, "kv_append_traffic_qwen3-8b_mixed.json")
+GATHER_TRAFFIC = os.path.join(PROFILES, "gather_kv_traffic_qwen3-8b_mixed.json")
+LONG_DECODE_TRAFFIC = os.path.join(PROFILES, "paged_decode_long_traffic_qwen3-8b.json")
 
 
 def measured_traffic(path: str):
@@ -599,7 +604,7 @@ def run_qk_norm_rope(args) -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(QK_TRAFFIC),
             "kernel": "qk_norm_rope_kernel",
             "bytes_per_launch": nbytes,
             "us_per_launch": round(us, 3),
@@ -725,7 +730,7 @@ def run_greedy(args) -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(GREEDY_TRAFFIC),
             "kernel": "greedy_argmax_kernel",
             "bytes_per_launch": nbytes,
             "us_per_launch": round(us, 3),
@@ -928,7 +933,8 @@ def _graph_time(torch, fn, launches: int, replays: int, warmup: int) -> float:
     return start.elapsed_time(end) / replays / launches * 1e3
 
 
-def _hbm_line(metric, achieved, us, nbytes, kernel, args, data, config, cpu=None):
+def _hbm_line(metric, achieved, us, nbytes, kernel, args, data, config, cpu=None,
+              traffic=None):
     result = {
         "metric": metric,
         "value": round(achieved, 1),
@@ -949,7 +955,7 @@ def _hbm_line(metric, achieved, us, nbytes, kernel, args, data, config, cpu=None
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "kernel": kernel,
             "bytes_per_launch": int(nbytes),
             "us_per_launch": round(us, 3),
@@ -1025,7 +1031,8 @@ def run_append(args) -> int:
                       "128, bf16, head-major pool of 65536 blocks of 16, distinct random slots; "
                       "20 launches replayed from a hipGraph, time per launch"),
          "tokens": tokens, "decode_append_us": round(small_us, 3),
-         "decode_append": "32 rows (the 0.6B decode step), same pool, launch-bound"}, cpu)
+         "decode_append": "32 rows (the 0.6B decode step), same pool, launch-bound"}, cpu,
+        measured_traffic(APPEND_TRAFFIC))
 
 
 def run_gather(args) -> int:
@@ -1090,7 +1097,7 @@ def run_gather(args) -> int:
         {"workload": ("gather of all 32 requests of the mixed chunked-prefill step (8 x 512 "
                       "chunks on prefixes U[0,3072] + 24 decode rows, U[256,2048]) into "
                       "contiguous K/V, 8 KV heads x 128, bf16, pool 65536 blocks of 16, one "
-                      "launch"), "rows": total}, cpu)
+                      "launch"), "rows": total}, cpu, measured_traffic(GATHER_TRAFFIC))
 
 
 def run_long_decode(args) -> int:
@@ -1159,7 +1166,7 @@ def run_long_decode(args) -> int:
     return _hbm_line("long-context paged decode HBM GB/s (% peak)", achieved, us, nbytes,
                      "paged_attention_vector_kernel (split + in-launch merge)", args,
                      "synthetic: seeded N(0,1) Q and pools, random distinct block tables",
-                     config, cpu)
+                     config, cpu, measured_traffic(LONG_DECODE_TRAFFIC))
 
 
 def main() -> int:
@@ -1198,22 +1205,20 @@ def main() -> int:
         return 2
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    standalone = {"qk-norm-rope": run_qk_norm_rope, "greedy": run_greedy,
+                  "engine": run_engine, "append": run_append, "gather": run_gather,
+                  "long-decode": run_long_decode}
+    if args.workload in standalone:
+        rc = standalone[args.workload](args)
+        if args.copy_calibration_mib:
+            import torch
+
+            copy_calibration(torch, args.copy_calibration_mib)
+        return rc
     if args.workload == "prefill":
         return run_prefill(args)
     if args.workload == "step-metadata":
         return run_step_metadata(args)
-    if args.workload == "qk-norm-rope":
-        return run_qk_norm_rope(args)
-    if args.workload == "greedy":
-        return run_greedy(args)
-    if args.workload == "engine":
-        return run_engine(args)
-    if args.workload == "append":
-        return run_append(args)
-    if args.workload == "gather":
-        return run_gather(args)
-    if args.workload == "long-decode":
-        return run_long_decode(args)
 
     import torch
 

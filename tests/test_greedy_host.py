@@ -41,3 +41,28 @@ def test_c_entry_validates_before_launch():
     assert _call(lib, state=8196) == 3
     assert _call(lib, rows=0) == 0  # nothing to do
     assert _lib.last_error() == ""
+
+
+def test_sampler_validation_matches_the_reference_contract():
+    # microinfer/layer/sampler.py:10-31: shape, temperature and logits checks
+    # run before any device work.
+    from microinfer_amd.layer.hip_sampler import Sampler
+
+    sampler = Sampler()
+    good = torch.zeros(2, 5)
+    temps = torch.ones(2)
+    with pytest.raises(ValueError, match="floating"):
+        sampler.probabilities(torch.zeros(2, 5, dtype=torch.int64), temps)
+    with pytest.raises(ValueError, match="temperature shape"):
+        sampler.probabilities(good, torch.ones(3))
+    with pytest.raises(ValueError, match="finite and positive"):
+        sampler.probabilities(good, torch.tensor([1.0, 0.0]))
+    with pytest.raises(ValueError, match="NaN"):
+        sampler.probabilities(torch.tensor([[0.0, float("nan")], [0.0, 1.0]]), temps)
+    with pytest.raises(ValueError, match="finite values"):
+        sampler.probabilities(torch.full((2, 3), float("-inf")), temps)
+    p = sampler.probabilities(torch.tensor([[0.0, 1.0, 2.0], [5.0, 5.0, 5.0]]),
+                              torch.tensor([1.0, 0.5]))
+    torch.testing.assert_close(p.sum(-1), torch.ones(2))
+    torch.testing.assert_close(p[1], torch.full((3,), 1 / 3))
+    assert p[0].argmax() == 2
