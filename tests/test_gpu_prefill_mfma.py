@@ -158,7 +158,7 @@ def test_contiguous_kv_matches_dense(dtype):
 
 
 def test_long_prefix_chunk():
-    # One 512-row chunk on a 3000-token prefix (the cfg4 shape of one request).
+    # One 512-row chunk on a 3000-token prefix (one request of the mixed prefill step).
     q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case([512], [3000], 32, 8, 16,
                                                           torch.bfloat16, 6)
     out = _run(q, kc, vc, tables, cu_q, cu_k)
