@@ -10,7 +10,8 @@ part only at a position whose top-2 logit gap in the oracle is below the
 tolerance (only there may other rounding flip the choice), after which the
 continuations differ. Chunked prefill, mixed steps, prefix-cache reuse
 and preemption must not change any token. A Qwen3-0.6B-shaped bfloat16 layer
-stack (MFMA prefill) is checked the same way with a wider gap tolerance.
+stack (MFMA prefill), and the full 28-layer Qwen3-0.6B of the engine
+workload, are checked the same way with a wider gap tolerance.
 """
 
 import numpy as np
@@ -129,3 +130,16 @@ def test_engine_rejects_requests_beyond_capacity(tiny_model):
     engine = make_engine(tiny_model, debug_mode=True, max_model_len=32)
     with pytest.raises(ValueError):
         engine.add_request(Sequence(list(range(40)), GREEDY))
+
+
+def test_qwen3_06b_engine_matches_oracle():
+    # The engine workload's model itself: Qwen3-0.6B dimensions (28 layers,
+    # vocabulary 151936), bf16, N(0, 0.02) weights, seed 0; four prompts of
+    # the workload's kind, four greedy tokens each. The oracle recomputes
+    # every sequence densely on the host (about 4 s per prompt).
+    model = Qwen3Model(QwenConfig(), dtype=torch.bfloat16, device="cuda", seed=0)
+    engine = make_engine(model, num_blocks=256, max_num_batched_tokens=512,
+                         max_num_prefill_tokens=512)
+    batch = prompts(5, [128, 64, 17, 100], vocab=151936)
+    out = engine.generate(batch, SampleParameter(max_tokens=4, greedy=True))
+    assert check_against_oracle(model, batch, out, 4, 0.03) >= 12
