@@ -279,6 +279,26 @@ def run_prefill(args) -> int:
     flops = prefill_flops(batch.q_lens, batch.context_lens, num_q_heads=32, head_dim=128)
     tflops = flops / (ms * 1e-3) / 1e12
     log(f"{ms * 1e3:.1f} us per launch, {tflops:.1f} TFLOP/s")
+    # Beside it, the no-prefix (direct) prefill on contiguous K/V: 8 prompts
+    # of 512 tokens, the same kernel without a block table.
+    d_lens = np.full(8, 512, dtype=np.int32)
+    d_cu = torch.tensor(np.concatenate([[0], np.cumsum(d_lens)]).astype(np.int32), device=dev)
+    d_rows = int(d_lens.sum())
+    dq = torch.randn((d_rows, 32, 128), generator=gen, device=dev).to(torch.bfloat16)
+    dk = torch.randn((d_rows, 8, 128), generator=gen, device=dev).to(torch.bfloat16)
+    dv = torch.randn((d_rows, 8, 128), generator=gen, device=dev).to(torch.bfloat16)
+    direct = lambda: hip_paged_prefill(dq, dk, dv, d_cu, d_cu, None, max_seqlen_q=512,  # noqa: E731
+                                       scale=scale)
+    for _ in range(max(1, args.warmup)):
+        direct()
+    start.record()
+    for _ in range(args.steps):
+        direct()
+    end.record()
+    torch.cuda.synchronize()
+    d_ms = start.elapsed_time(end) / args.steps
+    d_flops = prefill_flops(d_lens, d_lens, num_q_heads=32, head_dim=128)
+    log(f"direct prefill: {d_ms * 1e3:.1f} us per launch, {d_flops / d_ms / 1e9:.1f} TFLOP/s")
     result = {
         "metric": "paged chunked-prefill attention TFLOP/s (% of bf16 dense MFMA peak)",
         "value": round(tflops, 2),
@@ -302,6 +322,10 @@ def run_prefill(args) -> int:
             "query_rows": total_q,
             "flops_per_launch": flops,
             "kv_layout": args.layout,
+            "direct_prefill_us": round(d_ms * 1e3, 3),
+            "direct_prefill_tflops": round(d_flops / d_ms / 1e9, 2),
+            "direct_prefill": ("no-prefix prefill of 8 prompts x 512 tokens on contiguous K/V "
+                               "(no block table), same heads, one launch"),
         },
         "roofline": {
             "bound": "mfma",
