@@ -95,13 +95,21 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(
   }
   const R* w = is_q ? q_weight : k_weight;
   const V wa = load_pack<R, VEC>(w + oa), wb = load_pack<R, VEC>(w + ob);
+  // The angles as 16-byte vectors (the tables are 16-byte aligned and a
+  // lane's VEC angles start at a multiple of 4 floats).
+  static_assert(VEC % 4 == 0, "angles load as whole float4 vectors");
   const float* crow = cos_t + (pos_ok ? pos : 0) * HALF + j * VEC;
   const float* srow = sin_t + (pos_ok ? pos : 0) * HALF + j * VEC;
   float cs[VEC], sn[VEC];
 #pragma unroll
-  for (int k = 0; k < VEC; ++k) {
-    cs[k] = pos_ok ? crow[k] : 0.f;
-    sn[k] = pos_ok ? srow[k] : 0.f;
+  for (int k = 0; k < VEC; k += 4) {
+    const Pack<float, 4> c4 = load_pack<float, 4>(crow + k);
+    const Pack<float, 4> s4 = load_pack<float, 4>(srow + k);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      cs[k + i] = pos_ok ? c4.v[i] : 0.f;
+      sn[k + i] = pos_ok ? s4.v[i] : 0.f;
+    }
   }
   // Pair k of this lane: (x[k], y[k]) = (first, second) element of the pair.
   float x[VEC], y[VEC];
@@ -248,6 +256,7 @@ extern "C" int32_t mi_qk_norm_rope_append(
   }
   auto misaligned = [](const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 != 0; };
   if (misaligned(qkv) || misaligned(q_weight) || misaligned(k_weight) || misaligned(q_out) ||
+      misaligned(cos_table) || misaligned(sin_table) ||
       (k_out && misaligned(k_out)) ||
       (slot_mapping && (misaligned(key_cache) || misaligned(value_cache))) ||
       qkv_token_stride % vec || q_out_token_stride % vec || q_out_head_stride % vec ||
