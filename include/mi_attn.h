@@ -304,8 +304,8 @@ int32_t mi_step_metadata(const int32_t* cu_seqlens_q, const int32_t* starts,
  * int64 (positions_int64); a position outside [0, table_len) yields zero rows
  * in q_out / k_out and no append. head_dim is a power of two from two 16-byte
  * vectors (16 elements for bf16/f16, 8 for fp32) to 256; qkv, q_out, k_out,
- * the caches and the weights are 16-byte aligned, and every row and head
- * stride is a whole number of 16-byte vectors.
+ * the caches, the weights and the cos/sin tables are 16-byte aligned, and
+ * every row and head stride is a whole number of 16-byte vectors.
  */
 int32_t mi_qk_norm_rope_append(const void* qkv, int64_t qkv_token_stride, const void* q_weight,
                                const void* k_weight, float eps, const float* cos_table,

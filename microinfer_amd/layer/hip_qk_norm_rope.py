@@ -101,6 +101,8 @@ def qk_norm_rope_append(
     if tokens == 0:
         return (q, k) if return_k else q
     cos_table, sin_table = cos_table.contiguous(), sin_table.contiguous()
+    if cos_table.data_ptr() % 16 or sin_table.data_ptr() % 16:  # angles load as float4
+        cos_table, sin_table = cos_table.clone(), sin_table.clone()
     positions = positions.contiguous()
     q_weight, k_weight = q_weight.contiguous(), k_weight.contiguous()
     appending = slot_mapping is not None

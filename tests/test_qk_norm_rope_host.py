@@ -40,6 +40,7 @@ def test_c_entry_validates_before_launch():
     assert _call(lib, qkv=None) == 1 and "null" in _lib.last_error()
     assert _call(lib, ts=32) == 1 and "stride" in _lib.last_error()
     assert _call(lib, qkv=1032) == 1 and "aligned" in _lib.last_error()
+    assert _call(lib, cos=1028) == 1 and "aligned" in _lib.last_error()
     assert _call(lib, q_hs=20) == 1 and "aligned" in _lib.last_error()
     assert _call(lib, slots=1024) == 1 and "caches" in _lib.last_error()
     assert _call(lib, slots=1024, kc=1024, vc=1024) == 1 and "cache sizes" in _lib.last_error()
