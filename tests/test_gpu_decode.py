@@ -101,9 +101,13 @@ def test_decode_batch32_workload(layout):
     assert max_abs(out, expected) <= 2e-2
 
 
-@pytest.mark.parametrize("num_seqs,context", [(1, 4096), (4, 4096), (1, 32768), (4, 16384)])
+@pytest.mark.parametrize(
+    "num_seqs,context",
+    [(1, 4096), (1, 16384), (1, 32768), (4, 4096), (4, 16384), (4, 32768)],
+)
 def test_long_context_split_decode(num_seqs, context):
-    # 8B shape (32 Q / 8 KV heads), bf16, pool 65536 blocks, fixed contexts.
+    # 8B shape (32 Q / 8 KV heads), bf16, pool 65536 blocks, fixed contexts:
+    # every point of the long-context grid (1 or 4 sequences x 4K / 16K / 32K).
     batch = make_decode_batch(num_seqs=num_seqs, ctx_lo=context, ctx_hi=context,
                               pool_blocks=65536, draw_pools=False, **QWEN3_8B)
     cache = KVCache(1, 65536, 16, 8, 128, dtype=torch.bfloat16, device=DEV)
