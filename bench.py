@@ -11,7 +11,12 @@ last-level cache). The step is captured in a hipGraph and replayed; inputs
 are resident in HBM before timing.
 
 Prints one JSON line: value = whole-step algorithmic HBM bytes / step time
-(GB/s), the roofline of the decode launch and a CPU-oracle baseline.
+(GB/s), the roofline of the decode launch and a CPU-oracle baseline. The same
+line carries the other half of the metric: decode tok/s (and output tok/s) of
+the engine workload -- random-init Qwen3-0.6B serving 64 requests x 128
+prompt ids -> 16 greedy tokens -- in ``config.decode_tok_s``, with the same
+engine's decode on the host CPU (a KV-cached paged float32 forward under the
+same scheduler) in ``cpu_baseline_engine`` / ``config.cpu_decode_tok_s``.
 """
 
 from __future__ import annotations
@@ -29,6 +34,13 @@ import numpy as np
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def capture_graph(graph, pool=None, stream=None):
+    """The product's garbage-collector-safe graph capture (microinfer_amd.runner)."""
+    from microinfer_amd.runner import capture_graph as capture
+
+    return capture(graph, pool, stream)
 
 
 def log(msg: str) -> None:
@@ -293,7 +305,7 @@ def run_prefill(args) -> int:
     # launch would add its own gap (--graph measures that).
     if args.graph:
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        with capture_graph(graph):
             step()
         run = graph.replay
     else:
@@ -629,7 +641,7 @@ def run_qk_norm_rope(args) -> int:
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with capture_graph(graph):
         for _ in range(28):
             dec()
     for _ in range(args.warmup):
@@ -748,7 +760,7 @@ def run_greedy(args) -> int:
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=side):
+    with capture_graph(graph, stream=side):
         for _ in range(20):
             run()
     for _ in range(args.warmup):
@@ -828,39 +840,39 @@ def greedy_cpu_baseline(logits, nbytes, runs: int = 5):
     }
 
 
-def run_engine(args) -> int:
-    """The engine on random-init Qwen3-0.6B (28 layers, bf16): 64 requests of
-    128 uniform-random prompt ids arriving together, greedy, 16 output tokens
-    each, ignoring EOS; block 16, 4096 blocks, decode from hipGraph buckets,
-    mixed batches, max_num_seqs 64, max_num_batched_tokens 4096,
-    max_num_prefill_tokens 512. A step of the bench is one such batch run to
-    completion (fresh prompts each time)."""
+def measure_engine(batches: int, warmup: int) -> dict:
+    """The engine workload (``microinfer_amd.workloads``: random-init
+    Qwen3-0.6B, bf16, 64 requests x 128 uniform-random prompt ids arriving
+    together, 16 greedy tokens each, block 16, 4096 blocks, hipGraph decode,
+    mixed batches): ``batches`` batches run to completion after ``warmup``
+    untimed ones, fresh prompts each time.
+
+    Output tok/s = output tokens / wall time of the batches
+    (microinfer bench/online.py:81-91 semantics); decode tok/s = tokens of
+    decode-only steps / the time of those steps."""
     import torch
 
     from microinfer_amd.engine.blockmanager import BlockManager
-    from microinfer_amd.engine.config import EngineConfig, SampleParameter
     from microinfer_amd.engine.llm_engine import LLMEngine
     from microinfer_amd.engine.model import QwenConfig, Qwen3Model
     from microinfer_amd.engine.model_runner import ModelRunner
     from microinfer_amd.engine.scheduler import Scheduler
     from microinfer_amd.engine.sequence import Sequence
+    from microinfer_amd.workloads import (ENGINE_BLOCK_SIZE, ENGINE_NUM_BLOCKS,
+                                          ENGINE_OUTPUT_LEN, ENGINE_REQUESTS, engine_config,
+                                          engine_prompts, engine_sampling)
 
-    requests, prompt_len, out_len = 64, 128, 16
-    config = EngineConfig(max_num_seqs=64, max_num_batched_tokens=4096,
-                          max_num_prefill_tokens=512, max_model_len=4096,
-                          use_cuda_graph=True, mixed_batch=True)
-    model_config = QwenConfig()
-    log("building random-init Qwen3-0.6B and capturing decode graphs")
-    model = Qwen3Model(model_config, dtype=torch.bfloat16, device="cuda", seed=0)
-    runner = ModelRunner(model, config, num_blocks=4096, block_size=16)
-    manager = BlockManager(4096, 16)
+    config = engine_config()
+    log("building random-init Qwen3-0.6B for the engine workload")
+    model = Qwen3Model(QwenConfig(), dtype=torch.bfloat16, device="cuda", seed=0)
+    runner = ModelRunner(model, config, num_blocks=ENGINE_NUM_BLOCKS,
+                         block_size=ENGINE_BLOCK_SIZE)
+    manager = BlockManager(ENGINE_NUM_BLOCKS, ENGINE_BLOCK_SIZE)
     engine = LLMEngine(Scheduler(config, manager), runner)
-    params = SampleParameter(max_tokens=out_len, ignore_eos=True, greedy=True)
+    params = engine_sampling()
 
     def one_batch(seed):
-        rng = np.random.default_rng(seed)
-        seqs = [Sequence(rng.integers(0, model_config.vocab_size, prompt_len).tolist(), params)
-                for _ in range(requests)]
+        seqs = [Sequence(p, params) for p in engine_prompts(seed, model.config.vocab_size)]
         for seq in seqs:
             engine.add_request(seq)
         decode_s, decode_tokens, steps = 0.0, 0, 0
@@ -874,62 +886,72 @@ def run_engine(args) -> int:
                 decode_tokens -= num_tokens
             steps += 1
         wall = time.perf_counter() - start
-        assert all(len(s.completion_token_ids) == out_len for s in seqs)
+        assert all(len(s.completion_token_ids) == ENGINE_OUTPUT_LEN for s in seqs)
+        manager.reset_prefix_cache()
         return wall, decode_s, decode_tokens, steps
 
-    for i in range(max(1, args.warmup)):
+    for i in range(max(1, warmup)):
         one_batch(1000 + i)
-        manager.reset_prefix_cache()
     walls, decodes, dec_tokens, steps = [], [], 0, 0
-    for i in range(args.steps):
+    for i in range(batches):
         wall, dec_s, dec_tok, n = one_batch(i)
-        manager.reset_prefix_cache()
         walls.append(wall)
         decodes.append(dec_s)
         dec_tokens += dec_tok
         steps += n
-    output_tps = requests * out_len * args.steps / sum(walls)
+    output_tps = ENGINE_REQUESTS * ENGINE_OUTPUT_LEN * batches / sum(walls)
     decode_tps = dec_tokens / sum(decodes)
-    decode_step_us = sum(decodes) / (dec_tokens / requests) * 1e6 if dec_tokens else 0.0
-    # A full decode step streams every weight once (28 layers of QKV, output,
-    # gate/up and down projections, the norms and the untied vocabulary
-    # projection) plus the batch's K/V: bytes per step over the step time.
-    c = model_config
+    decode_steps = dec_tokens / ENGINE_REQUESTS
+    decode_step_us = sum(decodes) / decode_steps * 1e6 if dec_tokens else 0.0
+    log(f"engine: {output_tps:.0f} output tok/s over {batches} batches "
+        f"({statistics.mean(walls) * 1e3:.1f} ms each), decode {decode_tps:.0f} tok/s, "
+        f"{decode_step_us:.0f} us per decode step")
+    return dict(model=model, output_tps=output_tps, decode_tps=decode_tps,
+                decode_step_us=decode_step_us, wall_ms=statistics.mean(walls) * 1e3,
+                steps_per_batch=steps / batches, batches=batches, warmup=max(1, warmup))
+
+
+def engine_step_bytes(c, requests: int, mean_ctx: float) -> int:
+    """Bytes a full decode step streams: every weight once (28 layers of QKV,
+    output, gate/up and down products, the norms, the untied vocabulary
+    product) plus the batch's K/V."""
     per_layer = ((c.num_q_head + 2 * c.num_kv_head) * c.head_dim * c.hidden_dim
                  + c.hidden_dim * c.num_q_head * c.head_dim
                  + 3 * c.MLP_inter_dim * c.hidden_dim + 2 * c.hidden_dim + 2 * c.head_dim)
     weight_bytes = 2 * (c.num_hidden_layer * per_layer + c.vocab_size * c.hidden_dim
                         + c.hidden_dim)
-    mean_ctx = prompt_len + out_len / 2
     kv_bytes = 2 * 2 * c.num_hidden_layer * requests * mean_ctx * c.num_kv_head * c.head_dim
-    step_bytes = weight_bytes + kv_bytes
-    achieved = step_bytes / (decode_step_us * 1e-6) / 1e9 if decode_step_us else 0.0
-    log(f"{output_tps:.0f} output tok/s over {args.steps} batches "
-        f"({statistics.mean(walls) * 1e3:.1f} ms each), decode {decode_tps:.0f} tok/s, "
-        f"{decode_step_us:.0f} us per decode step")
+    return int(weight_bytes + kv_bytes)
+
+
+def run_engine(args) -> int:
+    """The engine workload; a bench step is one batch run to completion."""
+    from microinfer_amd.workloads import ENGINE_OUTPUT_LEN, ENGINE_PROMPT_LEN, ENGINE_REQUESTS
+
+    e = measure_engine(args.steps, args.warmup)
+    step_bytes = engine_step_bytes(e["model"].config, ENGINE_REQUESTS,
+                                   ENGINE_PROMPT_LEN + ENGINE_OUTPUT_LEN / 2)
+    us = e["decode_step_us"]
+    achieved = step_bytes / (us * 1e-6) / 1e9 if us else 0.0
     result = {
         "metric": "engine output tokens/s (random-init Qwen3-0.6B, 64 x 128-token prompts, "
                   "16 greedy outputs)",
-        "value": round(output_tps, 1),
+        "value": round(e["output_tps"], 1),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": max(1, args.warmup),
-        "ms_per_step": round(statistics.mean(walls) * 1e3, 3),
+        "warmup": e["warmup"],
+        "ms_per_step": round(e["wall_ms"], 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: random-init weights N(0, 0.02) (seed 0), uniform-random prompt ids",
         "config": {
-            "workload": ("engine: 64 requests x 128 random prompt ids arriving together, "
-                         "greedy, 16 output tokens (EOS ignored), Qwen3-0.6B random init, "
-                         "block 16, 4096 blocks, hipGraph decode, mixed batches, "
-                         "max_num_seqs 64, max_num_batched_tokens 4096, "
-                         "max_num_prefill_tokens 512; a bench step is one batch to completion"),
-            "decode_tokens_per_s": round(decode_tps, 1),
-            "decode_step_us": round(decode_step_us, 1),
-            "engine_steps_per_batch": steps / args.steps,
+            "workload": ENGINE_WORKLOAD_TEXT + "; a bench step is one batch to completion",
+            "decode_tokens_per_s": round(e["decode_tps"], 1),
+            "decode_step_us": round(us, 1),
+            "engine_steps_per_batch": e["steps_per_batch"],
         },
         "roofline": {
             "bound": "hbm",
@@ -941,34 +963,71 @@ def run_engine(args) -> int:
             "kernel": "decode step (hipGraph replay: 28 layers of GEMMs, fused Q/K norm + "
                       "RoPE + append, paged decode; vocabulary projection; argmax), host "
                       "time included",
-            "bytes_per_launch": int(step_bytes),
-            "us_per_launch": round(decode_step_us, 1),
+            "bytes_per_launch": step_bytes,
+            "us_per_launch": round(us, 1),
         },
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = engine_cpu_baseline(model, prompt_len)
+        result["cpu_baseline"] = engine_cpu_baseline(e["model"])
     print(json.dumps(result), flush=True)
     return 0
 
 
-def engine_cpu_baseline(model, prompt_len, new_tokens: int = 2):
-    """The dense oracle on the host: one request's 128-token prompt and
-    ``new_tokens`` greedy tokens, each recomputing the whole sequence."""
-    from oracle.qwen3_dense import greedy_generate
+ENGINE_WORKLOAD_TEXT = (
+    "engine: random-init Qwen3-0.6B (bf16, weights N(0, 0.02), seed 0), 64 requests x 128 "
+    "uniform-random prompt ids arriving together, greedy, 16 output tokens (EOS ignored), "
+    "block 16, 4096 blocks, hipGraph decode, mixed batches, max_num_seqs 64, "
+    "max_num_batched_tokens 4096, max_num_prefill_tokens 512")
 
-    weights = model.host_weights()
-    prompt = np.random.default_rng(99).integers(0, model.config.vocab_size, prompt_len).tolist()
+
+def engine_cpu_baseline(model, decode_steps: int = 5) -> dict:
+    """The same engine on the host: the product's Scheduler and BlockManager
+    drive a KV-cached paged float32 forward (oracle/qwen3_paged_host.py:
+    numpy GEMMs, the oracle's Q/K norm + RoPE + append into a paged cache and
+    its paged attention) over the workload's first batch; the prefill steps
+    run untimed, then ``decode_steps`` batch-64 decode steps are timed."""
+    from microinfer_amd.engine.blockmanager import BlockManager
+    from microinfer_amd.engine.llm_engine import LLMEngine
+    from microinfer_amd.engine.scheduler import Scheduler
+    from microinfer_amd.engine.sequence import Sequence
+    from microinfer_amd.workloads import (ENGINE_BLOCK_SIZE, ENGINE_NUM_BLOCKS, engine_config,
+                                          engine_prompts, engine_sampling)
+    from oracle.qwen3_paged_host import HostPagedRunner
+
+    log("CPU baseline: host paged engine over the workload's first batch")
+    runner = HostPagedRunner(model.host_weights(), model.config, ENGINE_NUM_BLOCKS,
+                             ENGINE_BLOCK_SIZE)
+    engine = LLMEngine(Scheduler(engine_config(), BlockManager(ENGINE_NUM_BLOCKS,
+                                                                ENGINE_BLOCK_SIZE)), runner)
+    for prompt in engine_prompts(0, model.config.vocab_size):
+        engine.add_request(Sequence(prompt, engine_sampling()))
     t0 = time.perf_counter()
-    greedy_generate(weights, model.config, prompt, new_tokens)
-    sec = time.perf_counter() - t0
+    prefill_s, prefill_steps = 0.0, 0
+    while True:  # prompt and mixed steps until the first decode-only step
+        t = time.perf_counter()
+        _, num_tokens = engine.step()
+        if num_tokens < 0:
+            break
+        prefill_s += time.perf_counter() - t
+        prefill_steps += 1
+    times, tokens = [], 0
+    for _ in range(decode_steps):
+        t = time.perf_counter()
+        _, num_tokens = engine.step()
+        times.append(time.perf_counter() - t)
+        tokens -= num_tokens
+    total = time.perf_counter() - t0
     return {
-        "value": round(new_tokens / sec, 3),
-        "unit": "tokens/s",
+        "value": round(tokens / sum(times), 2),
+        "unit": "decode tokens/s",
         "cores": blas_threads(),
         "kind": "port",
-        "sample": f"1 request, {prompt_len}-token prompt, {new_tokens} greedy tokens by the "
-                  f"dense numpy oracle (full recompute per token, float32/float64), "
-                  f"{sec:.1f} s on the host CPU ({cpu_model()})",
+        "sample": (f"first batch of the engine workload: {prefill_steps} prompt/mixed steps "
+                   f"untimed ({prefill_s:.1f} s), then {decode_steps} decode steps of "
+                   f"{tokens // decode_steps} rows timed ({sum(times):.2f} s); float32 numpy "
+                   f"KV-cached paged forward (oracle.qwen3_paged_host) under the product's "
+                   f"Scheduler/BlockManager, {total:.1f} s in all, on the host CPU "
+                   f"({cpu_model()}, os.cpu_count()={os.cpu_count()})"),
     }
 
 
@@ -982,7 +1041,7 @@ def _graph_time(torch, fn, launches: int, replays: int, warmup: int) -> float:
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=side):
+    with capture_graph(graph, stream=side):
         fn()
     for _ in range(max(1, warmup)):
         graph.replay()
@@ -1242,6 +1301,9 @@ def main() -> int:
     parser.add_argument("--layers", type=int, default=28)
     parser.add_argument("--layout", default="head_major", choices=["head_major", "token_major"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-engine", action="store_true",
+                        help="decode: leave out the engine half of the line (decode tok/s of "
+                             "the Qwen3-0.6B engine workload), e.g. for kernel profiling")
     parser.add_argument("--workload", default="decode",
                         choices=["decode", "prefill", "step-metadata", "qk-norm-rope",
                                  "greedy", "engine", "append", "gather", "long-decode"],
@@ -1283,6 +1345,36 @@ def main() -> int:
     if args.workload == "step-metadata":
         return run_step_metadata(args)
 
+    result = measure_decode(args)
+    if args.no_engine:
+        print(json.dumps(result), flush=True)
+        return 0
+    import torch
+
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()  # the 28 decode caches (30 GB) are gone
+    # The other half of the headline metric: decode tok/s of the engine
+    # workload, with its host counterpart beside it.
+    e = measure_engine(ENGINE_BATCHES, 1)
+    cfg = result["config"]
+    cfg["decode_tok_s"] = round(e["decode_tps"], 1)
+    cfg["engine_output_tok_s"] = round(e["output_tps"], 1)
+    cfg["engine_decode_step_us"] = round(e["decode_step_us"], 1)
+    cfg["engine_workload"] = (ENGINE_WORKLOAD_TEXT + f"; {ENGINE_BATCHES} batches timed after "
+                              "1 untimed, fresh prompts each")
+    if not args.no_cpu_baseline:
+        cpu = engine_cpu_baseline(e["model"])
+        cfg["cpu_decode_tok_s"] = cpu["value"]
+        result["cpu_baseline_engine"] = cpu
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+ENGINE_BATCHES = 3
+
+
+def measure_decode(args) -> dict:
+    """The headline paged-decode line (without the engine half)."""
     import torch
 
     from microinfer_amd.layer.hip_paged_attention import decode_plan, hip_paged_decode
@@ -1322,7 +1414,7 @@ def main() -> int:
             step()
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=capture_stream):
+        with capture_graph(graph, stream=capture_stream):
             step()
         torch.cuda.synchronize()
         run = graph.replay
@@ -1394,8 +1486,7 @@ def main() -> int:
     if not args.no_cpu_baseline:
         log("timing the CPU oracle on layer 0")
         result["cpu_baseline"] = cpu_baseline(torch, state)
-    print(json.dumps(result), flush=True)
-    return 0
+    return result
 
 
 if __name__ == "__main__":

@@ -102,7 +102,8 @@ int32_t mi_kv_append(const void* keys, int64_t key_token_stride, int64_t key_hea
  * can serve all later calls on the same stream. Calls that run concurrently
  * (different streams) need separate counters and workspaces.
  * plan: NULL, or a plan from mi_decode_plan for this step (see there) in a
- * buffer of plan_bytes >= mi_decode_plan_bytes(...) under the current tuning.
+ * buffer of plan_bytes >= mi_decode_plan_bytes(...). When plan is NULL the
+ * call computes its plan first, and that launch also zeroes the counters.
  * Sequences with context_len 0 produce zeros.
  */
 int64_t mi_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
@@ -127,15 +128,6 @@ int64_t mi_decode_plan_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t spl
 int32_t mi_decode_plan(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
                        int32_t block_size, int32_t block_table_width, int32_t split_k,
                        void* plan, int64_t plan_bytes, void* stream);
-
-/*
- * Tuning of the adaptive partition plan (split_k = 0): aim for about
- * target_items (work item, KV head) workgroups per launch, each covering at
- * least min_part_blocks cache blocks. Values <= 0 leave a knob unchanged.
- * Process-wide; changes the size mi_paged_decode_workspace_bytes reports, so
- * set it before sizing workspaces or capturing graphs. Defaults 192 / 4.
- */
-void mi_tune_decode(int32_t target_items, int32_t min_part_blocks);
 
 int32_t mi_paged_decode(const void* query, int64_t q_token_stride, int64_t q_head_stride,
                         const void* key_cache, const void* value_cache,

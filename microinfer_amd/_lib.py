@@ -35,7 +35,6 @@ SIGNATURES = {
          _I32, _I32, _I32, _I32, _I32, _P],
     ),
     "mi_paged_decode_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I32]),
-    "mi_tune_decode": (None, [_I32, _I32]),
     "mi_paged_decode": (
         _I32,
         [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P, _P, _I64, _I64,

@@ -5,8 +5,8 @@
 // The reference fixes split_k per launch on the host from R * Hq
 // (microinfer/layer/triton_paged_attention.py:342-349) and stripes tiles over
 // the splits (:76-79). Here partitions are contiguous block ranges sized from
-// the step's total context: about target_items (item, KV head) workgroups of
-// at least min_part_blocks blocks each. Sequences are ordered longest first,
+// the step's total context: about kTargetItems (item, KV head) workgroups of
+// at least kMinPartBlocks blocks each. Sequences are ordered longest first,
 // so the partitions of split sequences run (and merge) early while shorter
 // single-partition items keep the memory system busy at the end.
 #include "paged_attention.h"
@@ -14,8 +14,11 @@
 namespace mi {
 namespace {
 
-int32_t g_target_items = 192;
-int32_t g_min_part_blocks = 4;
+// About this many (item, KV head) workgroups per launch, each covering at
+// least kMinPartBlocks cache blocks. Fixed: the plan's size, and so the
+// workspace a caller sizes, depends only on the call's arguments.
+constexpr int32_t kTargetItems = 192;
+constexpr int32_t kMinPartBlocks = 4;
 
 constexpr int kPlanThreads = 1024;
 constexpr int kSortLimit = 1024;  // larger batches keep submission order
@@ -33,7 +36,7 @@ __device__ __forceinline__ int part_blocks(int nb, int split_k, int pb_global) {
 __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
     const int32_t* __restrict__ context_lens, int num_seqs, int num_kv_heads, int block_size,
     int lb, int width, int split_k, int target, int min_pb, int max_items,
-    PlanItem* __restrict__ plan) {
+    PlanItem* __restrict__ plan, int32_t* __restrict__ counters, int num_counters) {
   __shared__ int s_ctx[kMaxPlanSeqs];
   __shared__ int s_order[kMaxPlanSeqs];  // rank -> sequence
   __shared__ int s_first[kMaxPlanSeqs];  // rank -> first item index
@@ -43,6 +46,11 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
   const int tid = threadIdx.x;
   const int max_ctx = width * block_size;
 
+  // Arrival counters of the decode launch that follows (when given): zero
+  // them here, so a caller whose counter memory is shared or reused needs
+  // no separate clear.
+  if (counters != nullptr)
+    for (int i = tid; i < num_counters; i += kPlanThreads) counters[i] = 0;
   if (tid == 0) {
     s_total_blocks = 0;
     s_total_items = 0;
@@ -139,7 +147,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
 
 int32_t decode_max_items(int32_t num_seqs, int32_t num_kv_heads, int32_t split_k) {
   if (split_k > 0) return num_seqs * split_k;
-  return (g_target_items + num_kv_heads - 1) / num_kv_heads + num_seqs;
+  return (kTargetItems + num_kv_heads - 1) / num_kv_heads + num_seqs;
 }
 
 int64_t decode_plan_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t split_k) {
@@ -149,20 +157,16 @@ int64_t decode_plan_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t split_
 
 int32_t launch_decode_plan(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
                            int32_t block_size, int32_t block_table_width, int32_t split_k,
-                           PlanItem* plan, hipStream_t stream) {
+                           PlanItem* plan, int32_t* counters, hipStream_t stream) {
   decode_plan_kernel<<<1, kPlanThreads, 0, stream>>>(
       context_lens, num_seqs, num_kv_heads, block_size, ilog2(block_size), block_table_width,
-      split_k, g_target_items, g_min_part_blocks,
-      decode_max_items(num_seqs, num_kv_heads, split_k), plan);
+      split_k, kTargetItems, kMinPartBlocks,
+      decode_max_items(num_seqs, num_kv_heads, split_k), plan, counters,
+      counters != nullptr ? num_seqs * num_kv_heads : 0);
   return check_launch("decode plan");
 }
 
 }  // namespace mi
-
-extern "C" void mi_tune_decode(int32_t target_items, int32_t min_part_blocks) {
-  if (target_items > 0) mi::g_target_items = target_items;
-  if (min_part_blocks > 0) mi::g_min_part_blocks = min_part_blocks;
-}
 
 extern "C" int64_t mi_decode_plan_bytes(int32_t num_seqs, int32_t num_kv_heads,
                                         int32_t split_k) {
@@ -189,6 +193,6 @@ extern "C" int32_t mi_decode_plan(const int32_t* context_lens, int32_t num_seqs,
       reinterpret_cast<uintptr_t>(plan) % 32 != 0)
     return fail(MI_ERR_WORKSPACE, "mi_decode_plan: plan buffer too small or misaligned");
   return launch_decode_plan(context_lens, num_seqs, num_kv_heads, block_size,
-                            block_table_width, split_k, static_cast<PlanItem*>(plan),
+                            block_table_width, split_k, static_cast<PlanItem*>(plan), nullptr,
                             static_cast<hipStream_t>(stream));
 }

@@ -42,8 +42,6 @@ struct AttnArgs {
   int32_t max_q;     // varlen: no request has more query rows (launch shape)
   int32_t num_kv_heads, group, head_dim, block_size, log2_block, num_blocks;
   int32_t split_k;          // 0 = adaptive partitions
-  int32_t target_items;     // adaptive: aim for about this many (item, head) groups
-  int32_t min_part_blocks;  // adaptive: smallest partition, in blocks
   int32_t max_items;        // grid.x of the decode launch
   float scale_log2;         // softmax scale * log2(e)
   int32_t varlen;
@@ -65,10 +63,33 @@ int32_t decode_max_items(int32_t num_seqs, int32_t num_kv_heads, int32_t split_k
 // Plan size and launch (decode_plan.hip). The plan has decode_max_items()
 // entries; unused ones carry seq = -1.
 int64_t decode_plan_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t split_k);
+// counters (optional): the (sequence, KV head) arrival counters of the
+// decode launch that follows, zeroed by the plan kernel.
 int32_t launch_decode_plan(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
                            int32_t block_size, int32_t block_table_width, int32_t split_k,
-                           PlanItem* plan, hipStream_t stream);
+                           PlanItem* plan, int32_t* counters, hipStream_t stream);
 
 constexpr int32_t kMaxPlanSeqs = 4096;
+
+// The step's new K/V rows for the fused append (all null: no append).
+struct NewRows {
+  const void* keys = nullptr;
+  int64_t k_ts = 0, k_hs = 0;
+  const void* values = nullptr;
+  int64_t v_ts = 0, v_hs = 0;
+};
+
+// Validated decode (paged_attention.hip), shared by the C entry points:
+// mi_paged_decode, mi_paged_decode_append and the allocation-free variant.
+int32_t paged_decode(
+    const void* query, int64_t q_token_stride, int64_t q_head_stride, const void* key_cache,
+    const void* value_cache, int64_t cache_block_stride, int64_t cache_token_stride,
+    int64_t cache_head_stride, const int32_t* block_tables, int64_t block_table_stride,
+    int32_t block_table_width, const int32_t* context_lens, void* out,
+    int64_t out_token_stride, int64_t out_head_stride, void* workspace,
+    int64_t workspace_bytes, int32_t* counters, const void* plan, int64_t plan_bytes,
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t block_size, int32_t num_blocks, int32_t split_k, float scale, int32_t dtype,
+    const NewRows& rows, void* stream);
 
 }  // namespace mi

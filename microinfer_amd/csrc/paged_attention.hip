@@ -71,15 +71,6 @@ extern "C" int64_t mi_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num
 }
 
 namespace mi {
-namespace {
-
-// The step's new K/V rows for the fused append (all null: no append).
-struct NewRows {
-  const void* keys = nullptr;
-  int64_t k_ts = 0, k_hs = 0;
-  const void* values = nullptr;
-  int64_t v_ts = 0, v_hs = 0;
-};
 
 int32_t paged_decode(
     const void* query, int64_t q_token_stride, int64_t q_head_stride, const void* key_cache,
@@ -168,9 +159,11 @@ int32_t paged_decode(
   char* ws = static_cast<char*>(workspace);
   const int64_t plan_region = round_up(decode_plan_bytes(num_seqs, num_kv_heads, split_k), 256);
   if (plan == nullptr) {
+    // The plan kernel also zeroes the counters this launch uses.
     PlanItem* own = reinterpret_cast<PlanItem*>(ws);
     st = launch_decode_plan(context_lens, num_seqs, num_kv_heads, block_size,
-                            block_table_width, split_k, own, s);
+                            block_table_width, split_k, own, partials > 0 ? counters : nullptr,
+                            s);
     if (st != MI_OK) return st;
     a.plan = own;
   } else {
@@ -186,7 +179,6 @@ int32_t paged_decode(
   return dispatch_vector(a, dtype, s);
 }
 
-}  // namespace
 }  // namespace mi
 
 extern "C" int32_t mi_paged_decode(

@@ -23,6 +23,8 @@ A scheduled sequence is any object with ``len()``, slicing over its token ids,
 
 from __future__ import annotations
 
+import contextlib
+import gc
 from itertools import chain
 
 import numpy as np
@@ -33,6 +35,28 @@ from microinfer_amd.layer.hip_sampler import greedy_argmax
 from microinfer_amd.layer.metadata import AttentionMetadata
 
 _INT32_MAX = 2 ** 31 - 1
+
+
+@contextlib.contextmanager
+def capture_graph(graph, pool=None, stream=None):
+    """``torch.cuda.graph(graph, pool, stream=stream)`` with Python's cyclic
+    garbage collector kept off for the whole capture.
+
+    Objects that hold graphs (a runner whose graph runner calls back into it
+    forms a reference cycle) are freed only by that collector; if it ran
+    during a capture, destroying such a graph would be a HIP call that is
+    illegal while a stream captures, and the process would abort. So collect
+    what is already garbage first, then capture with the collector disabled
+    (torch's own capture no longer collects by default)."""
+    gc.collect()
+    enabled = gc.isenabled()
+    gc.disable()
+    try:
+        with torch.cuda.graph(graph, pool, stream=stream):
+            yield
+    finally:
+        if enabled:
+            gc.enable()
 
 
 def graph_buckets(max_num_seqs: int) -> list[int]:
@@ -373,7 +397,7 @@ class DecodeGraphRunner:
         # created during the warm-up (the decode arrival counters, the argmax
         # row slots) is reused rather than allocated and zero-filled inside
         # the graph.
-        with torch.cuda.graph(graph, self.pool, stream=side), torch.inference_mode():
+        with capture_graph(graph, self.pool, stream=side), torch.inference_mode():
             out = self._step(ids, positions, buffers.metadata(batch))
         if self.pool is None:
             self.pool = graph.pool()

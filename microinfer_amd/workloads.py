@@ -193,3 +193,39 @@ def prefill_flops(q_lens, contexts, *, num_q_heads, head_dim) -> int:
         prefix = c - q
         total += 4 * num_q_heads * head_dim * (q * prefix + q * (q + 1) // 2)
     return int(total)
+
+
+# The engine workload: random-init Qwen3-0.6B serving 64 requests of 128
+# uniform-random prompt ids that arrive together, greedy, 16 output tokens
+# each (EOS ignored); block 16, 4096 blocks, decode replayed from hipGraph
+# buckets, mixed (decode-first) batches, max_num_seqs 64,
+# max_num_batched_tokens 4096, max_num_prefill_tokens 512 -- the limits of
+# the reference's published online run (docs/p4.md:172-176).
+ENGINE_REQUESTS = 64
+ENGINE_PROMPT_LEN = 128
+ENGINE_OUTPUT_LEN = 16
+ENGINE_NUM_BLOCKS = 4096
+ENGINE_BLOCK_SIZE = 16
+
+
+def engine_config(**overrides):
+    from microinfer_amd.engine.config import EngineConfig
+
+    values = dict(max_num_seqs=64, max_num_batched_tokens=4096, max_num_prefill_tokens=512,
+                  max_model_len=4096, use_cuda_graph=True, mixed_batch=True)
+    values.update(overrides)
+    return EngineConfig(**values)
+
+
+def engine_prompts(seed: int, vocab_size: int, requests: int = ENGINE_REQUESTS,
+                   prompt_len: int = ENGINE_PROMPT_LEN) -> list[list[int]]:
+    """One batch of the engine workload: ``requests`` prompts of uniform-random
+    ids in [0, vocab_size), drawn one request after another from PCG64(seed)."""
+    rng = np.random.default_rng(seed)
+    return [rng.integers(0, vocab_size, prompt_len).tolist() for _ in range(requests)]
+
+
+def engine_sampling():
+    from microinfer_amd.engine.config import SampleParameter
+
+    return SampleParameter(max_tokens=ENGINE_OUTPUT_LEN, ignore_eos=True, greedy=True)

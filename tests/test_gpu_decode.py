@@ -18,8 +18,9 @@ import pytest
 import torch
 
 from microinfer_amd.layer.hip_paged_attention import hip_paged_decode
-from microinfer_amd.workloads import QWEN3_06B, QWEN3_8B, make_decode_batch
+from microinfer_amd.runner import capture_graph
 from microinfer_amd.worker.kv_cache import KVCache
+from microinfer_amd.workloads import QWEN3_06B, QWEN3_8B, make_decode_batch
 from oracle import kv_append
 from tests.support import (
     TOLERANCE,
@@ -282,7 +283,7 @@ def test_hipgraph_replay_tracks_new_contexts():
     hip_paged_decode(q, kc, vc, tables, lens)  # warm-up outside capture
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with capture_graph(graph):
         out.copy_(hip_paged_decode(q, kc, vc, tables, lens))
     for step, new in enumerate([[11, 501, 1001, 2001], [1, 2048, 17, 300], [700, 700, 700, 700]]):
         lens.copy_(torch.tensor(new, dtype=torch.int32))

@@ -14,8 +14,9 @@ import pytest
 import torch
 
 from microinfer_amd.layer.hip_paged_attention import decode_plan, hip_paged_decode
-from microinfer_amd.workloads import QWEN3_06B, QWEN3_8B, make_decode_batch
+from microinfer_amd.runner import capture_graph
 from microinfer_amd.worker.kv_cache import KVCache
+from microinfer_amd.workloads import QWEN3_06B, QWEN3_8B, make_decode_batch
 from oracle import kv_append
 from tests.support import TOLERANCE, bits, max_abs, oracle_decode, rounded
 
@@ -145,7 +146,7 @@ def test_fused_append_reuses_plan_across_layers_and_graph_replay():
     step()
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with capture_graph(graph):
         step()
     for replay, new in enumerate([[6, 101, 301, 641, 18, 34], [7, 102, 302, 642, 19, 35]]):
         lens.copy_(torch.tensor(new, dtype=torch.int32))

@@ -18,7 +18,7 @@ import torch
 
 from microinfer_amd.layer import hip_sampler
 from microinfer_amd.layer.hip_sampler import greedy_argmax
-from microinfer_amd.runner import DecodeGraphRunner, StepMetadataBuilder
+from microinfer_amd.runner import DecodeGraphRunner, StepMetadataBuilder, capture_graph
 from oracle.greedy import greedy_argmax as oracle_argmax
 from tests.support import FakeSeq
 from tests.test_gpu_step_metadata import _attention_forward
@@ -123,7 +123,7 @@ def test_graph_replays_select_each_new_batch():
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=side):
+    with capture_graph(graph, stream=side):
         tokens = greedy_argmax(logits)
     for replay in range(5):
         fresh = _with_ties(rows, vocab, torch.bfloat16, 500 + replay)

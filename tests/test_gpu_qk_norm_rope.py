@@ -19,6 +19,7 @@ import pytest
 import torch
 
 from microinfer_amd.layer.hip_qk_norm_rope import qk_norm_rope_append
+from microinfer_amd.runner import capture_graph
 from oracle import qk_norm_rope as ref
 from tests.support import as_f32
 
@@ -201,7 +202,7 @@ def test_graph_replay_with_new_positions_and_slots():
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with capture_graph(graph):
         out.copy_(step(kc, vc))
     kc_e, vc_e = kc.clone(), vc.clone()  # after the warm-up's writes
     gen = torch.Generator().manual_seed(11)

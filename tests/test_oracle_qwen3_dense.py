@@ -7,6 +7,12 @@
 * Appending tokens never changes the logits of earlier positions (causality).
 * ``causal_attention`` equals the explicit-loop float64 attention.
 * ``greedy_generate`` appends the argmax of the last row each step.
+* ``teacher_forced`` on the greedy completion gives back exactly the greedy
+  tokens and gaps; on any other completion each choice equals the argmax of
+  a separate full forward over the prefix before it; widening the weights
+  once (``weights_f64``) and projecting only the last rows change no bit;
+  ``token_deficits`` is zero on the greedy path and, for the runner-up
+  token, equals the top-2 gap.
 """
 
 from types import SimpleNamespace
@@ -16,7 +22,8 @@ import torch
 from torch.nn import functional as F
 
 from oracle.paged_attention import dense_causal_attention_f64
-from oracle.qwen3_dense import causal_attention, forward_logits, greedy_generate
+from oracle.qwen3_dense import (causal_attention, forward_logits, greedy_generate,
+                                teacher_forced, token_deficits, top2_gap, weights_f64)
 
 CFG = SimpleNamespace(vocab_size=96, hidden_dim=64, norm_eps=1e-6, MLP_inter_dim=96,
                       num_q_head=4, num_kv_head=2, head_dim=16, num_hidden_layer=2,
@@ -117,3 +124,52 @@ def test_greedy_generate_appends_last_row_argmax():
         seq.append(tok)
     cut, _ = greedy_generate(w, CFG, prompt, 4, eos=out[1])
     assert cut == out[:2]
+
+
+def test_teacher_forced_on_the_greedy_path_is_greedy_generation():
+    w = make_weights(CFG, seed=4)
+    prompt = [5, 9, 2, 7]
+    out, gaps = greedy_generate(w, CFG, prompt, 5)
+    picks, tf_gaps = teacher_forced(w, CFG, prompt, out)
+    assert picks == out
+    np.testing.assert_allclose(tf_gaps, gaps, rtol=0, atol=1e-12)
+
+
+def test_teacher_forced_checks_every_position_of_another_path():
+    w = make_weights(CFG, seed=5)
+    prompt = [1, 2, 3]
+    completion = [10, 20, 30, 40]  # not the greedy path
+    picks, gaps = teacher_forced(w, CFG, prompt, completion)
+    assert len(picks) == len(gaps) == len(completion)
+    for i in range(len(completion)):
+        row = forward_logits(w, CFG, prompt + completion[:i])[-1]
+        assert picks[i] == int(np.argmax(row))
+        assert gaps[i] == top2_gap(row)
+    assert teacher_forced(w, CFG, prompt, []) == ([], [])
+
+
+def test_wide_weights_and_last_rows_change_nothing():
+    w = make_weights(CFG, seed=6)
+    ids = [3, 1, 4, 1, 5, 9, 2, 6]
+    full = forward_logits(w, CFG, ids)
+    wide = forward_logits(weights_f64(w), CFG, ids)
+    assert np.array_equal(full, wide)
+    assert np.array_equal(forward_logits(w, CFG, ids, last_rows=3), full[-3:])
+    assert top2_gap(np.array([1.0, 4.0, 2.5])) == 1.5 and top2_gap(np.array([2.0])) == float("inf")
+
+
+def test_token_deficits():
+    w = make_weights(CFG, seed=7)
+    prompt = [2, 7, 1]
+    out, gaps = greedy_generate(w, CFG, prompt, 4)
+    assert token_deficits(w, CFG, prompt, out) == [0.0] * 4
+    row = forward_logits(w, CFG, prompt)[-1]
+    runner_up = int(np.argsort(row)[-2])
+    # (the products run over different row counts here, so agreement is to
+    # float64 rounding, not bitwise)
+    np.testing.assert_allclose(token_deficits(w, CFG, prompt, [runner_up]), [gaps[0]],
+                               rtol=1e-12)
+    worst = int(np.argmin(row))
+    np.testing.assert_allclose(token_deficits(w, CFG, prompt, [worst]),
+                               [row.max() - row.min()], rtol=1e-12)
+    assert token_deficits(w, CFG, prompt, []) == []
