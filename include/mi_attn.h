@@ -181,6 +181,34 @@ int32_t mi_paged_decode_append(const void* new_keys, int64_t nk_token_stride,
                                float scale, int32_t dtype, void* stream);
 
 /*
+ * Allocation-free variant of mi_paged_decode_append, for callers that cannot
+ * allocate device memory (code under hipGraph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). It has no counterpart in the reference.
+ *
+ * Same arguments, rules and result as mi_paged_decode_append with
+ * workspace/counters/plan omitted and plan = NULL: its plan, split partials
+ * and arrival counters live in a static device array of the library
+ * (32 MiB per GPU, held until the process ends). The call fails with
+ * MI_ERR_WORKSPACE when mi_paged_decode_workspace_bytes(...) for its sizes
+ * exceeds mi_paged_decode_noalloc_max_bytes(), and with MI_ERR_UNSUPPORTED
+ * past 4096 sequences or 16 KV heads. No hipMalloc, hipFree or memset: the
+ * plan launch zeroes the counters this call uses. Every call on one GPU
+ * shares that GPU's array, so calls that may overlap on one GPU (different
+ * streams, or host threads racing on one) race on it; serialise them.
+ */
+int64_t mi_paged_decode_noalloc_max_bytes(void);
+int32_t mi_paged_decode_append_noalloc(
+    const void* new_keys, int64_t nk_token_stride, int64_t nk_head_stride,
+    const void* new_values, int64_t nv_token_stride, int64_t nv_head_stride,
+    const void* query, int64_t q_token_stride, int64_t q_head_stride, void* key_cache,
+    void* value_cache, int64_t cache_block_stride, int64_t cache_token_stride,
+    int64_t cache_head_stride, const int32_t* block_tables, int64_t block_table_stride,
+    int32_t block_table_width, const int32_t* context_lens, void* out,
+    int64_t out_token_stride, int64_t out_head_stride, int32_t num_seqs,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+    int32_t num_blocks, int32_t split_k, float scale, int32_t dtype, void* stream);
+
+/*
  * Paged varlen (prefill / mixed) attention with a bottom-right causal mask:
  * request r owns query rows [cu_seqlens_q[r], cu_seqlens_q[r+1]) and context
  * c_r = cu_seqlens_k[r+1] - cu_seqlens_k[r]; its query row i sits at position

@@ -46,6 +46,13 @@ SIGNATURES = {
          _P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P, _P, _I64, _I64,
          _P, _I64, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P],
     ),
+    "mi_paged_decode_noalloc_max_bytes": (_I64, []),
+    "mi_paged_decode_append_noalloc": (
+        _I32,
+        [_P, _I64, _I64, _P, _I64, _I64,
+         _P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P, _P, _I64, _I64,
+         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P],
+    ),
     "mi_qk_norm_rope_append": (
         _I32,
         [_P, _I64, _P, _P, _F32, _P, _P, _I32, _P, _I32, _P, _P, _I64, _I64, _P, _I64, _I64,
