@@ -17,8 +17,20 @@ namespace {
 // About this many (item, KV head) workgroups per launch, each covering at
 // least kMinPartBlocks cache blocks. Fixed: the plan's size, and so the
 // workspace a caller sizes, depends only on the call's arguments.
-constexpr int32_t kTargetItems = 192;
-constexpr int32_t kMinPartBlocks = 4;
+#ifndef MI_PLAN_TARGET
+#define MI_PLAN_TARGET 192
+#endif
+#ifndef MI_PLAN_EQUAL
+#define MI_PLAN_EQUAL 0
+#endif
+#ifndef MI_PLAN_ORDER
+#define MI_PLAN_ORDER 0
+#endif
+#ifndef MI_PLAN_MIN_PART
+#define MI_PLAN_MIN_PART 4
+#endif
+constexpr int32_t kTargetItems = MI_PLAN_TARGET;
+constexpr int32_t kMinPartBlocks = MI_PLAN_MIN_PART;
 
 constexpr int kPlanThreads = 1024;
 constexpr int kSortLimit = 1024;  // larger batches keep submission order
@@ -28,7 +40,11 @@ __device__ __forceinline__ int blocks_of(int ctx, int block_size, int lb) {
 }
 
 __device__ __forceinline__ int part_blocks(int nb, int split_k, int pb_global) {
-  if (split_k == 0) return pb_global;
+  if (split_k == 0) {
+    if (!MI_PLAN_EQUAL) return pb_global;
+    const int np = max(1, (nb + pb_global - 1) / pb_global);
+    return max(1, (nb + np - 1) / np);
+  }
   const int k = min(split_k, max(nb, 1));
   return max(1, (nb + k - 1) / k);
 }
@@ -75,10 +91,12 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
   for (int r = tid; r < num_seqs; r += kPlanThreads) {
     int rank = r;
     if (sort) {
-      const int nb = blocks_of(s_ctx[r], block_size, lb);
+      int nb = blocks_of(s_ctx[r], block_size, lb);
+      if (MI_PLAN_ORDER == 1) nb = part_blocks(nb, split_k, pb_global);
       rank = 0;
       for (int s = 0; s < num_seqs; ++s) {
-        const int ns = blocks_of(s_ctx[s], block_size, lb);
+        int ns = blocks_of(s_ctx[s], block_size, lb);
+        if (MI_PLAN_ORDER == 1) ns = part_blocks(ns, split_k, pb_global);
         rank += (ns > nb) || (ns == nb && s < r);
       }
     }

@@ -96,6 +96,33 @@ __device__ __forceinline__ void pin(Pack<R, N>& p) {
   p = __builtin_bit_cast(Pack<R, N>, w);
 }
 
+// Direct global->LDS load of 16 bytes per lane: lane i's bytes land at
+// lds_dst + 16 i (global_load_lds_dwordx4, LDS base in M0; one wait state
+// between the M0 write and the load). Issued as inline assembly so that the
+// compiler does not track it: its own wait insertion would otherwise wait for
+// these loads before every LDS read. The kernel waits for them explicitly
+// (vmcnt) and orders them with bare barriers.
+__device__ __forceinline__ void lds_load16(const void* src, const void* lds_dst) {
+  const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (const __attribute__((address_space(3))) void*)(lds_dst)));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds)
+               : "memory", "m0");
+}
+
+// The same load with a scalar base and a per-lane 32-bit byte offset
+// (saddr form), which saves the per-lane 64-bit address arithmetic.
+__device__ __forceinline__ void lds_load16_sbase(const void* base, uint32_t byte_off,
+                                                 const void* lds_dst) {
+  const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (const __attribute__((address_space(3))) void*)(lds_dst)));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(byte_off), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+
 template <typename R, int N>
 __device__ __forceinline__ Pack<R, N> zero_pack() {
   Pack<R, N> z;

@@ -57,6 +57,11 @@ int32_t launch_paged_attention_vector(const AttnArgs& args, int32_t dtype,
 bool prefill_mfma_supported(const AttnArgs& args, int32_t dtype);
 int32_t launch_prefill_mfma(const AttnArgs& args, int32_t dtype, hipStream_t stream);
 
+// MFMA decode kernel (paged_decode_mfma.hip): 16-bit caches, head_dim 128,
+// up to 16 query heads per KV head, block size >= 16, paged.
+bool decode_mfma_supported(const AttnArgs& args, int32_t dtype);
+int32_t launch_decode_mfma(const AttnArgs& args, int32_t dtype, hipStream_t stream);
+
 // Upper bound on decode work items for a launch (grid.x / Hkv).
 int32_t decode_max_items(int32_t num_seqs, int32_t num_kv_heads, int32_t split_k);
 

@@ -176,6 +176,7 @@ int32_t paged_decode(
     a.ws_ml = a.ws_acc + acc_floats;
     a.counters = counters;
   }
+  if (decode_mfma_supported(a, dtype)) return launch_decode_mfma(a, dtype, s);
   return dispatch_vector(a, dtype, s);
 }
 

@@ -104,21 +104,6 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 using LdsShort4 = __attribute__((address_space(3))) short4_t;
 using LdsVoid = __attribute__((address_space(3))) void;
 
-// Direct global->LDS load of 16 bytes per lane: lane i's bytes land at
-// lds_dst + 16 i (global_load_lds_dwordx4, LDS base in M0; one wait state
-// between the M0 write and the load). Issued as inline assembly so that the
-// compiler does not track it: its own wait insertion would otherwise wait for
-// these loads before every LDS read. The kernel waits for them explicitly
-// (vmcnt) and orders them with bare barriers.
-__device__ __forceinline__ void lds_load16(const void* src, const void* lds_dst) {
-  const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-      (const __attribute__((address_space(3))) void*)(lds_dst)));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(src), "s"(lds)
-               : "memory", "m0");
-}
-
 // Four 16-bit elements, transposed across each group of 16 lanes
 // (ds_read_b64_tr_b16): lane l of a group receives element l % 4 of the
 // 8-byte rows read by lanes l / 4, l / 4 + 4, l / 4 + 8 and l / 4 + 12.
