@@ -1286,7 +1286,7 @@ def run_long_decode(args) -> int:
               "cases_gbs": {k: round(v[1] / v[0] / 1e3, 1) for k, v in cases.items()},
               "note": "1 x 4096 (16.8 MB) is launch-latency-bound"}
     return _hbm_line("long-context paged decode HBM GB/s (% peak)", achieved, us, nbytes,
-                     "paged_attention_vector_kernel (split + in-launch merge)", args,
+                     "paged_decode_mfma_kernel (split + in-launch merge)", args,
                      "synthetic: seeded N(0,1) Q and pools, random distinct block tables",
                      config, cpu, measured_traffic(LONG_DECODE_TRAFFIC))
 
@@ -1476,7 +1476,7 @@ def measure_decode(args) -> dict:
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(DECODE_TRAFFIC),
-            "kernel": "paged_attention_vector_kernel (fused append + decode + split merge)",
+            "kernel": "paged_decode_mfma_kernel (fused append + decode + split merge)",
             "bytes_per_launch": layer_bytes,
             "us_per_launch": round(layer_us, 3),
             "timing": "HIP events around the timed steps / (steps x layers); includes the "

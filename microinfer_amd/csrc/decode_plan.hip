@@ -17,20 +17,8 @@ namespace {
 // About this many (item, KV head) workgroups per launch, each covering at
 // least kMinPartBlocks cache blocks. Fixed: the plan's size, and so the
 // workspace a caller sizes, depends only on the call's arguments.
-#ifndef MI_PLAN_TARGET
-#define MI_PLAN_TARGET 192
-#endif
-#ifndef MI_PLAN_EQUAL
-#define MI_PLAN_EQUAL 0
-#endif
-#ifndef MI_PLAN_ORDER
-#define MI_PLAN_ORDER 0
-#endif
-#ifndef MI_PLAN_MIN_PART
-#define MI_PLAN_MIN_PART 4
-#endif
-constexpr int32_t kTargetItems = MI_PLAN_TARGET;
-constexpr int32_t kMinPartBlocks = MI_PLAN_MIN_PART;
+constexpr int32_t kTargetItems = 192;
+constexpr int32_t kMinPartBlocks = 4;
 
 constexpr int kPlanThreads = 1024;
 constexpr int kSortLimit = 1024;  // larger batches keep submission order
@@ -40,11 +28,7 @@ __device__ __forceinline__ int blocks_of(int ctx, int block_size, int lb) {
 }
 
 __device__ __forceinline__ int part_blocks(int nb, int split_k, int pb_global) {
-  if (split_k == 0) {
-    if (!MI_PLAN_EQUAL) return pb_global;
-    const int np = max(1, (nb + pb_global - 1) / pb_global);
-    return max(1, (nb + np - 1) / np);
-  }
+  if (split_k == 0) return pb_global;
   const int k = min(split_k, max(nb, 1));
   return max(1, (nb + k - 1) / k);
 }
@@ -91,12 +75,10 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
   for (int r = tid; r < num_seqs; r += kPlanThreads) {
     int rank = r;
     if (sort) {
-      int nb = blocks_of(s_ctx[r], block_size, lb);
-      if (MI_PLAN_ORDER == 1) nb = part_blocks(nb, split_k, pb_global);
+      const int nb = blocks_of(s_ctx[r], block_size, lb);
       rank = 0;
       for (int s = 0; s < num_seqs; ++s) {
-        int ns = blocks_of(s_ctx[s], block_size, lb);
-        if (MI_PLAN_ORDER == 1) ns = part_blocks(ns, split_k, pb_global);
+        const int ns = blocks_of(s_ctx[s], block_size, lb);
         rank += (ns > nb) || (ns == nb && s < r);
       }
     }

@@ -124,28 +124,14 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
   using QWord = typename std::conditional<PAIRS, uint32_t, float>::type;
   const R* qbase = static_cast<const R*>(a.q) + q_row * a.q_ts + d0;
   QWord qv[GMAX][QW];
-  auto load_q = [&]() {
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g) {
-      Pack<R, VEC> qp = zero_pack<R, VEC>();
-      if (EXACT || g < G) qp = load_pack<R, VEC>(qbase + (head * G + g) * a.q_hs);
-      const Pack<QWord, QW> words = __builtin_bit_cast(Pack<QWord, QW>, qp);
+  for (int g = 0; g < GMAX; ++g) {
+    Pack<R, VEC> qp = zero_pack<R, VEC>();
+    if (EXACT || g < G) qp = load_pack<R, VEC>(qbase + (head * G + g) * a.q_hs);
+    const Pack<QWord, QW> words = __builtin_bit_cast(Pack<QWord, QW>, qp);
 #pragma unroll
-      for (int j = 0; j < QW; ++j) qv[g][j] = words.v[j];
-    }
-  };
-#ifndef MI_LDS_RING
-#define MI_LDS_RING 1
-#endif
-  // Ring mode (paged fast path, 8-wave workgroups): each wave stages its
-  // next two tiles in a private LDS ring with direct global->LDS loads, which
-  // the compiler does not track, and waits for them explicitly. Register
-  // loads would be made to wait for the previous tile before the next one is
-  // issued (the compiler's wait insertion is conservative around the loop),
-  // leaving about one tile per wave in flight.
-  constexpr bool RING = FAST && MI_LDS_RING && NW == 8;
-  // Ring mode loads the query after the first tile's loads are issued.
-  if constexpr (!RING) load_q();
+    for (int j = 0; j < QW; ++j) qv[g][j] = words.v[j];
+  }
   const float scale_log2 = a.scale_log2;
 
   float m[GMAX], lsum[GMAX], acc[GMAX][VEC];
@@ -281,78 +267,8 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
   // The next tile is issued unconditionally (past the end its loads hit the
   // safe row and are masked), so every path through the loop has the same
   // loads in flight and the wait counts stay exact.
-  constexpr int kLoadBytes = kWave * 16;            // one load instruction
-  constexpr int kSlotBytes = 2 * UNROLL * kLoadBytes;  // K then V of one tile
-  constexpr int kRingSlots = 2;
-  __shared__ __attribute__((aligned(16))) char s_ring[RING ? NW * kRingSlots * kSlotBytes : 16];
   constexpr int STRIDE = TILE * NW;
-  if constexpr (RING) {
-    char* my_ring = s_ring + wave * kRingSlots * kSlotBytes;
-    const R* kbase = kc + head_off;
-    const R* vbase = vc + head_off;
-    // Issue the tile at t0 into ring slot `slot`; returns its validity bits.
-    auto issue_ring = [&](int slot, int t0) -> uint32_t {
-      int ids[UNROLL];
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u) ids[u] = ctab[min((t0 + u * PPW) >> lb, last_blk)];
-      uint32_t ok = 0;
-      char* dst = my_ring + slot * kSlotBytes;
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u) {
-        const int p0 = t0 + u * PPW;
-        const int blk = ids[u];
-        const bool blk_ok = p0 < pos_end && blk >= 0 && blk < a.num_blocks;
-        const bool lane_ok = blk_ok && p0 + grp < pos_end;
-        // Masked loads read the head's first row of block 0 (in bounds).
-        const int64_t soff = blk_ok ? blk * a.c_bs + (p0 & bmask) * a.c_ts : 0;
-        const uint32_t loff = static_cast<uint32_t>(lane_ok ? lane_off : d0) * sizeof(R);
-        lds_load16_sbase(kbase + soff, loff, dst + u * kLoadBytes);
-        lds_load16_sbase(vbase + soff, loff, dst + (UNROLL + u) * kLoadBytes);
-        ok |= static_cast<uint32_t>(lane_ok) << u;
-      }
-      return ok;
-    };
-    // The query rows are loaded behind the first tile, then everything in
-    // flight is waited for once, so the compiler has no load of its own left
-    // to wait for inside the loop (where its wait would also drain the ring).
-    const bool has_tiles = pos_begin + wave * TILE < pos_end;
-    int t0 = pos_begin + wave * TILE;
-    uint32_t ok_slot[2] = {0, 0};
-    if (has_tiles) ok_slot[0] = issue_ring(0, t0);
-    load_q();
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (has_tiles) {
-      ok_slot[1] = issue_ring(1, t0 + STRIDE);
-      int slot = 0;
-      Tile T;
-      while (true) {
-        // The other slot's 2 * UNROLL loads may stay in flight.
-        static_assert(2 * UNROLL <= 15, "vmcnt field");
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * UNROLL));
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        const char* src = my_ring + slot * kSlotBytes + lane * 16;
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-          T.k[u] = *reinterpret_cast<const Pack<R, VEC>*>(src + u * kLoadBytes);
-          T.v[u] = *reinterpret_cast<const Pack<R, VEC>*>(src + (UNROLL + u) * kLoadBytes);
-        }
-        T.ok = slot ? ok_slot[1] : ok_slot[0];
-        // This wave's reads of the slot have returned before it is refilled.
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        const uint32_t okn = issue_ring(slot, t0 + 2 * STRIDE);
-        if (slot) ok_slot[1] = okn; else ok_slot[0] = okn;
-        consume(T);
-        if (t0 + STRIDE >= pos_end) break;
-        t0 += STRIDE;
-        slot ^= 1;
-      }
-      // No load may still be writing the ring when it is reused below.
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    }
-  } else if (pos_begin + wave * TILE < pos_end) {
+  if (pos_begin + wave * TILE < pos_end) {
     Tile A, B;
     int t0 = pos_begin + wave * TILE;
     issue(A, t0);
@@ -417,23 +333,13 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
 
   // Merge the NW wave states through LDS; wave 0 carries on alone.
   if constexpr (NW > 1) {
-    // In ring mode each wave's state goes into its own (drained) ring slots.
-    constexpr int kAccFloats = GMAX * D;
-    static_assert(!RING || kAccFloats * 4 <= kRingSlots * kSlotBytes, "state fits the ring");
-    __shared__ float s_acc_own[RING ? 1 : NW * kAccFloats];
+    __shared__ float s_acc[NW][GMAX][D];
     __shared__ float s_ml[NW][GMAX][2];
-    auto state_acc = [&](int wv) -> float* {
-      if constexpr (RING)
-        return reinterpret_cast<float*>(s_ring + wv * kRingSlots * kSlotBytes);
-      else
-        return s_acc_own + wv * kAccFloats;
-    };
     if (grp == 0) {
-      float* mine = state_acc(wave);
 #pragma unroll
       for (int g = 0; g < GMAX; ++g)
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) mine[g * D + d0 + j] = acc[g][j];
+        for (int j = 0; j < VEC; ++j) s_acc[wave][g][d0 + j] = acc[g][j];
     }
     if (lane == 0) {
 #pragma unroll
@@ -458,7 +364,7 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
         const float f = (mk == -INFINITY) ? 0.f : fast_exp2(mk - mx);
         l = fmaf(f, s_ml[k][g][1], l);
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) o[j] = fmaf(f, state_acc(k)[g * D + d0 + j], o[j]);
+        for (int j = 0; j < VEC; ++j) o[j] = fmaf(f, s_acc[k][g][d0 + j], o[j]);
       }
       m[g] = mx;
       lsum[g] = l;
@@ -617,21 +523,6 @@ constexpr int kWavesPerGroup = MI_WAVES_PER_GROUP;
 // instead of 15.6; 32 sequences, one 8-wave group per CU, stays faster.)
 constexpr int kNarrowWavesPerGroup = 4;
 
-// Compute units of the current device (cached per device).
-inline int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-      cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
-
 constexpr int tile_unroll(int gmax) {
   return gmax <= 2 ? MI_TILE_UNROLL_SMALL_GROUP : MI_TILE_UNROLL_LARGE_GROUP;
 }
@@ -644,10 +535,7 @@ int32_t launch_vector_typed(const AttnArgs& a, hipStream_t stream) {
   const int D = a.head_dim;
   const int G = a.group;
   const dim3 grid((a.varlen ? a.num_rows : a.max_items) * a.num_kv_heads);
-#ifndef MI_NARROW_MODE
-#define MI_NARROW_MODE 0
-#endif
-  const bool narrow = MI_NARROW_MODE == 1 ? !a.varlen : MI_NARROW_MODE == 2 ? false :
+  const bool narrow =
       !a.varlen && static_cast<int64_t>(a.num_seqs) * a.num_kv_heads > device_cus();
   bool launched = false;
 

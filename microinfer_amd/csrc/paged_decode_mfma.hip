@@ -87,7 +87,10 @@ constexpr int kSlotBytes = 2 * kHalfBytes;        // K then V
 constexpr int kLoadsPerHalf = kHalfBytes / kLoadBytes;  // 4
 constexpr int kLoadsPerTile = 2 * kLoadsPerHalf;        // 8
 constexpr int kRescaleSlack = 15;
-static_assert(kLoadsPerTile <= 15, "vmcnt immediate");
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt
+// bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+constexpr int vmcnt_only(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+static_assert(3 * kLoadsPerTile <= 63, "vmcnt immediate");
 
 // LDS tile rows are 256 bytes; the 16-byte chunk c of row r sits at chunk
 // position c ^ swz(r). K fragment reads (16 lanes: rows 0-15, one chunk
@@ -108,13 +111,14 @@ __device__ __forceinline__ float lane_xor32(float v, int lane) {
   return __builtin_bit_cast(float, lane < 32 ? r[1] : r[0]);
 }
 
-template <typename E, int NW>
+template <typename E, int NW, int NS>
 __global__ __launch_bounds__(kWave * NW) void paged_decode_mfma_kernel(const AttnArgs a) {
   using M = DecodeMfma<E>;
   using vec8 = typename M::vec8;
   using R = uint16_t;
   using ConstI32 = __attribute__((address_space(4))) const int32_t;
-  __shared__ __attribute__((aligned(16))) char s_ring[NW * 2 * kSlotBytes];
+  static_assert(NS >= 2 && NS <= 4, "ring depth");
+  __shared__ __attribute__((aligned(16))) char s_ring[NW * NS * kSlotBytes];
   __shared__ float s_m[NW][kHeads];
   __shared__ float s_l[NW][kHeads];
   __shared__ int s_arrived;
@@ -173,7 +177,7 @@ __global__ __launch_bounds__(kWave * NW) void paged_decode_mfma_kernel(const Att
     off_k[u] = static_cast<uint32_t>((row * c_ts + ((lane % 16) ^ swz_k(row)) * 8) * 2);
     off_v[u] = static_cast<uint32_t>((row * c_ts + ((lane % 16) ^ swz_v(row)) * 8) * 2);
   }
-  char* my_ring = s_ring + wave * 2 * kSlotBytes;
+  char* my_ring = s_ring + wave * NS * kSlotBytes;
 
   // Issue tile k's loads into ring slot `slot`; returns whether its block id
   // is valid (an invalid block reads block 0 and is masked).
@@ -269,9 +273,13 @@ __global__ __launch_bounds__(kWave * NW) void paged_decode_mfma_kernel(const Att
     for (int db = 0; db < kD / 16; ++db) o[db] = M::pv(vf[db], pf, o[db]);
   };
 
+  // Static interleave: wave w takes tiles w, w + NW, ...; NS ring slots per
+  // wave, so up to NS tiles of a wave are in flight.
   const int k0 = wave;
   if (k0 < ntiles) {
-    bool ok_slot[2] = {false, false};
+    bool ok_slot[NS];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) ok_slot[j] = false;
     ok_slot[0] = issue(0, k0);
     load_q();
     if (owner) {
@@ -282,16 +290,24 @@ __global__ __launch_bounds__(kWave * NW) void paged_decode_mfma_kernel(const Att
     }
     // Everything in flight (query, new row, first tile) is waited for once,
     // so the compiler has no load of its own left to wait for in the loop.
-    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (k0 + NW < ntiles) ok_slot[1] = issue(1, k0 + NW);
+#pragma unroll
+    for (int j = 1; j < NS; ++j)
+      if (k0 + j * NW < ntiles) ok_slot[j] = issue(j, k0 + j * NW);
     int k = k0, slot = 0;
     while (true) {
-      // Tile k is in this slot; tile k + NW (if any) was issued after it.
-      if (k + NW < ntiles)
-        __builtin_amdgcn_s_waitcnt(0x0F70 | kLoadsPerTile);
+      // Tile k is in this slot; the younger tiles k + j NW (j < NS) that
+      // exist were issued after it.
+      const int younger = min(NS - 1, (ntiles - 1 - k) / NW);
+      if (younger == 0)
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+      else if (younger == 1)
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(kLoadsPerTile));
+      else if (younger == 2)
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * kLoadsPerTile));
       else
-        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(3 * kLoadsPerTile));
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       char* cur = my_ring + slot * kSlotBytes;
       if (owner && k == append_tile) {
@@ -303,19 +319,24 @@ __global__ __launch_bounds__(kWave * NW) void paged_decode_mfma_kernel(const Att
                                          ((lane ^ swz_v(r)) * 16)) = new_v;
         }
       }
-      const bool cur_ok = slot ? ok_slot[1] : ok_slot[0];
+      bool cur_ok = ok_slot[0];
+#pragma unroll
+      for (int j = 1; j < NS; ++j)
+        if (slot == j) cur_ok = ok_slot[j];
       compute(k, cur, cur_ok);
       if (k + NW >= ntiles) break;
       // The fragment reads of this slot have returned (compute used them);
-      // refill it with tile k + 2 NW.
-      if (k + 2 * NW < ntiles) {
+      // refill it with tile k + NS NW.
+      if (k + NS * NW < ntiles) {
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        const bool okn = issue(slot, k + 2 * NW);
-        if (slot) ok_slot[1] = okn; else ok_slot[0] = okn;
+        const bool okn = issue(slot, k + NS * NW);
+#pragma unroll
+        for (int j = 0; j < NS; ++j)
+          if (slot == j) ok_slot[j] = okn;
       }
       k += NW;
-      slot ^= 1;
+      slot = slot + 1 == NS ? 0 : slot + 1;
     }
   } else {
     load_q();  // no tiles: the state stays empty
@@ -375,7 +396,7 @@ __global__ __launch_bounds__(kWave * NW) void paged_decode_mfma_kernel(const Att
         const float mw = s_m[wv][h];
         const float f = mw == -INFINITY ? 0.f : fast_exp2(mw - mx);
         ls = fmaf(f, s_l[wv][h], ls);
-        os = fmaf(f, reinterpret_cast<const float*>(s_ring + wv * 2 * kSlotBytes)[h * kD + d], os);
+        os = fmaf(f, reinterpret_cast<const float*>(s_ring + wv * NS * kSlotBytes)[h * kD + d], os);
       }
       acc_v[j] = os;
       m_v[j] = mx;
@@ -461,28 +482,14 @@ __global__ __launch_bounds__(kWave * NW) void paged_decode_mfma_kernel(const Att
 // Decode launches with more (sequence, KV head) pairs than the device has
 // CUs use 4-wave workgroups (64 KiB of LDS, two per CU) instead of one 8-wave
 // workgroup (128 KiB) per CU.
-int device_cus_mfma() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-      cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
-
 template <typename E>
 int32_t launch_typed(const AttnArgs& a, hipStream_t stream) {
   const dim3 grid(static_cast<uint32_t>(a.max_items) * a.num_kv_heads);
-  const bool narrow = static_cast<int64_t>(a.num_seqs) * a.num_kv_heads > device_cus_mfma();
+  const bool narrow = static_cast<int64_t>(a.num_seqs) * a.num_kv_heads > device_cus();
   if (narrow)
-    paged_decode_mfma_kernel<E, 4><<<grid, kWave * 4, 0, stream>>>(a);
+    paged_decode_mfma_kernel<E, 4, 2><<<grid, kWave * 4, 0, stream>>>(a);
   else
-    paged_decode_mfma_kernel<E, 8><<<grid, kWave * 8, 0, stream>>>(a);
+    paged_decode_mfma_kernel<E, 8, 2><<<grid, kWave * 8, 0, stream>>>(a);
   return check_launch("paged decode (MFMA)");
 }
 
