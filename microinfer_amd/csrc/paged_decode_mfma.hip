@@ -117,7 +117,7 @@ __global__ __launch_bounds__(kWave * NW) void paged_decode_mfma_kernel(const Att
   using vec8 = typename M::vec8;
   using R = uint16_t;
   using ConstI32 = __attribute__((address_space(4))) const int32_t;
-  static_assert(NS >= 2 && NS <= 4, "ring depth");
+  static_assert(NS >= 1 && NS <= 4, "ring depth (slots per wave)");
   __shared__ __attribute__((aligned(16))) char s_ring[NW * NS * kSlotBytes];
   __shared__ float s_m[NW][kHeads];
   __shared__ float s_l[NW][kHeads];
