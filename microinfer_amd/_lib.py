@@ -25,7 +25,8 @@ _I32 = ctypes.c_int32
 _I64 = ctypes.c_int64
 _F32 = ctypes.c_float
 
-# (restype, argtypes) of every entry point declared in include/mi_attn.h.
+# (restype, argtypes) of every entry point declared in include/mi_attn.h and
+# include/mi_model.h.
 SIGNATURES = {
     "mi_last_error": (ctypes.c_char_p, []),
     "mi_abi_version": (_I32, []),
@@ -77,6 +78,10 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _I64, _I32, _P, _P, _P, _P,
          _P],
     ),
+    "mi_linear": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I32, _I32, _I32, _I32, _P]),
+    "mi_rms_norm_residual": (
+        _I32, [_P, _I64, _P, _I64, _P, _F32, _P, _I64, _P, _I64, _I32, _I32, _I32, _P]),
+    "mi_silu_mul": (_I32, [_P, _I64, _P, _I64, _I32, _I32, _I32, _P]),
 }
 
 _lock = threading.Lock()

@@ -74,21 +74,6 @@ int32_t launch_decode_plan(const int32_t* context_lens, int32_t num_seqs, int32_
                            int32_t block_size, int32_t block_table_width, int32_t split_k,
                            PlanItem* plan, int32_t* counters, hipStream_t stream);
 
-// Compute units of the current device (cached per device).
-inline int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-      cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
-
 constexpr int32_t kMaxPlanSeqs = 4096;
 
 // The step's new K/V rows for the fused append (all null: no append).

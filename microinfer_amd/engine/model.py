@@ -11,8 +11,12 @@ last row on prefill (qwen3.py:57-65).
 
 On this path the per-layer Q/K norm + RoPE + KV append is one HIP launch
 (``mi_qk_norm_rope_append``), attention is the HIP paged decode / varlen
-prefill (``paged_attention_meta`` / ``varlen_attention``), and the dense
-products, RMSNorm and SwiGLU are torch (hipBLASLt). Weights are random:
+prefill (``paged_attention_meta`` / ``varlen_attention``), and RMSNorm with
+its residual sum and the SwiGLU gate are HIP launches too (``hip_dense``:
+the counterparts of the reference's compiled ``_compiled_add_rms_norm`` /
+``_compiled_swiglu``), as are the projections of small decode batches where
+the HIP product is measured faster than torch's (``prefer_hip_linear``); the
+rest stay on torch (hipBLASLt). Weights are random:
 N(0, 0.02) from a seeded generator, norm weights 1, since no checkpoint is
 available to load (``init_std`` sets the spread).
 """
@@ -24,6 +28,8 @@ from dataclasses import dataclass
 import torch
 from torch.nn import functional as F
 
+from microinfer_amd.layer.hip_dense import (hip_linear, hip_rms_norm_residual, hip_silu_mul,
+                                            prefer_hip_linear, supported_rows)
 from microinfer_amd.layer.hip_qk_norm_rope import qk_norm_rope_append, rope_tables
 from microinfer_amd.layer.paged_attention import paged_attention_meta, varlen_attention
 
@@ -61,7 +67,7 @@ class Qwen3Model:
     """Weights plus the packed-token forward over a bound KV cache."""
 
     def __init__(self, config: QwenConfig, *, dtype=torch.bfloat16, device="cuda", seed=0,
-                 init_std: float = 0.02):
+                 init_std: float = 0.02, hip_dense: bool = True):
         c = config
         if c.num_q_head % c.num_kv_head or c.head_dim % 2:
             raise ValueError("invalid GQA head ratio or RoPE dimension")
@@ -89,6 +95,7 @@ class Qwen3Model:
         self.cos, self.sin = rope_tables(c.max_pos_embed, c.head_dim, c.rope_base,
                                          device=self.device)
         self.caches = None
+        self.hip_dense = hip_dense and dtype in (torch.bfloat16, torch.float16)
 
     def bind_caches(self, caches) -> None:
         """One ``LayerKVCache`` per layer (``[N, B, Hkv, D]`` views)."""
@@ -97,8 +104,21 @@ class Qwen3Model:
         self.caches = list(caches)
 
     def _norm(self, x, residual, weight):
+        if self.hip_dense and supported_rows(x, residual):
+            return hip_rms_norm_residual(x, residual, weight, self.config.norm_eps)
         combined = x if residual is None else x + residual
         return F.rms_norm(combined, (combined.shape[-1],), weight, self.config.norm_eps), combined
+
+    def _linear(self, x, weight):
+        if self.hip_dense and prefer_hip_linear(x, weight):
+            return hip_linear(x, weight)
+        return F.linear(x, weight)
+
+    def _swiglu(self, gate_up):
+        if self.hip_dense and supported_rows(gate_up):
+            return hip_silu_mul(gate_up)
+        gate, up = gate_up.chunk(2, dim=-1)
+        return F.silu(gate) * up
 
     def forward(self, input_ids, positions, metadata):
         """Hidden states ``[T, H]`` of the packed tokens of one step."""
@@ -111,7 +131,7 @@ class Qwen3Model:
         hidden, residual = F.embedding(input_ids, self.embedding), None
         for layer, cache in zip(self.layers, self.caches):
             x, residual = self._norm(hidden, residual, layer.pre_norm)
-            qkv = F.linear(x, layer.qkv)
+            qkv = self._linear(x, layer.qkv)
             rotated = qk_norm_rope_append(
                 qkv, q_weight=layer.q_norm, k_weight=layer.k_norm, eps=c.norm_eps,
                 cos_table=self.cos, sin_table=self.sin, positions=positions,
@@ -124,10 +144,9 @@ class Qwen3Model:
                 attn = varlen_attention(q, k, v.contiguous(), metadata)
             else:
                 attn = paged_attention_meta(rotated, cache.keys, cache.values, metadata)
-            hidden = F.linear(attn.reshape(tokens, q_width), layer.out)
+            hidden = self._linear(attn.reshape(tokens, q_width), layer.out)
             x, residual = self._norm(hidden, residual, layer.post_norm)
-            gate, up = F.linear(x, layer.gate_up).chunk(2, dim=-1)
-            hidden = F.linear(F.silu(gate) * up, layer.down)
+            hidden = self._linear(self._swiglu(self._linear(x, layer.gate_up)), layer.down)
         return self._norm(hidden, residual, self.final_norm)[0]
 
     def compute_logits(self, hidden, metadata):
@@ -135,7 +154,7 @@ class Qwen3Model:
         row (decode)."""
         if metadata.is_prefill and metadata.cu_seqlens_q is not None:
             hidden = hidden[metadata.cu_seqlens_q[1:].long() - 1]
-        return F.linear(hidden, self.lm_head)
+        return self._linear(hidden, self.lm_head)
 
     def host_weights(self) -> dict:
         """float32 numpy copies of every weight, keyed as the dense oracle

@@ -1,4 +1,4 @@
-"""The C-ABI library loads and exports what include/mi_attn.h declares.
+"""The C-ABI library loads and exports what include/*.h declares.
 
 No kernel is launched here: argument validation returns before any HIP call,
 so these run on a host without a GPU.
@@ -12,12 +12,15 @@ import pytest
 
 from microinfer_amd import _lib
 
-HEADER = Path(__file__).resolve().parents[1] / "include" / "mi_attn.h"
+HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h"))
 
 
 def declared_functions():
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(mi_\w+)\s*\(", text, re.M)))
+    names = set()
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names |= set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(mi_\w+)\s*\(", text, re.M))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():
@@ -104,3 +107,30 @@ def test_workspace_size_formula(split_k):
     items = plan // 32
     partials = 0 if split_k == 1 else items * 8 * 4 * (128 + 2) * 4
     assert size == plan_region + partials
+
+
+def test_dense_ops_validate_before_launch():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(256)
+    # n not a multiple of 16, k not a multiple of 32
+    assert lib.mi_linear(fake, 1024, fake, 1024, fake, 1000, 8, 1000, 1024, 2, None) == 1
+    assert lib.mi_linear(fake, 1000, fake, 1000, fake, 1024, 8, 1024, 1000, 2, None) == 1
+    # more than 64 rows, or 32-bit elements: no kernel (the caller keeps torch)
+    assert lib.mi_linear(fake, 1024, fake, 1024, fake, 1024, 65, 1024, 1024, 2, None) == 2
+    assert lib.mi_linear(fake, 1024, fake, 1024, fake, 1024, 8, 1024, 1024, 0, None) == 2
+    # strides below the row lengths, misaligned rows
+    assert lib.mi_linear(fake, 512, fake, 1024, fake, 1024, 8, 1024, 1024, 2, None) == 1
+    assert lib.mi_linear(fake, 1028, fake, 1024, fake, 1024, 8, 1024, 1024, 2, None) == 1
+    assert "aligned" in _lib.last_error()
+    assert lib.mi_linear(None, 0, None, 0, None, 0, 0, 1024, 1024, 2, None) == 0
+    assert lib.mi_rms_norm_residual(fake, 1024, None, 0, fake, 1e-6, fake, 1024, None, 0, 4,
+                                    1020, 2, None) == 1
+    assert lib.mi_rms_norm_residual(fake, 1024, None, 0, fake, 1e-6, fake, 1024, None, 0, 4,
+                                    1024, 0, None) == 2
+    assert lib.mi_rms_norm_residual(fake, 16384, None, 0, fake, 1e-6, fake, 16384, None, 0, 4,
+                                    16384, 2, None) == 2
+    assert lib.mi_rms_norm_residual(None, 0, None, 0, None, 1e-6, None, 0, None, 0, 0, 1024,
+                                    2, None) == 0
+    assert lib.mi_silu_mul(fake, 6144, fake, 3072, 4, 3070, 2, None) == 1
+    assert lib.mi_silu_mul(fake, 6000, fake, 3072, 4, 3072, 2, None) == 1
+    assert lib.mi_silu_mul(None, 0, None, 0, 0, 3072, 2, None) == 0
