@@ -310,6 +310,26 @@ __global__ __launch_bounds__(kWave * NW) void paged_decode_mfma_kernel(const Att
         __builtin_amdgcn_s_waitcnt(vmcnt_only(3 * kLoadsPerTile));
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       char* cur = my_ring + slot * kSlotBytes;
+      bool cur_ok = ok_slot[0];
+#pragma unroll
+      for (int j = 1; j < NS; ++j)
+        if (slot == j) cur_ok = ok_slot[j];
+      {
+        // Rows past the context or of an invalid block hold whatever the
+        // cache holds there; their weights are 0, but 0 * NaN is NaN, so
+        // their V rows are zeroed in the tile (tail tiles only; K needs
+        // nothing, its scores are replaced by -inf).
+        const int p0 = pos_begin + k * kTile;
+        if (!cur_ok || p0 + kTile > pos_end) {
+          const int r = lane / 4;
+          if (!cur_ok || p0 + r >= pos_end) {
+            char* row = cur + kHalfBytes + r * kRowBytes + (lane % 4) * 64;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              *reinterpret_cast<Pack<uint32_t, 4>*>(row + c * 16) = zero_pack<uint32_t, 4>();
+          }
+        }
+      }
       if (owner && k == append_tile) {
         // The step's new row replaces the (stale) cache row in the tile.
         const int r = (ctx - 1) & (kTile - 1);
@@ -319,10 +339,6 @@ __global__ __launch_bounds__(kWave * NW) void paged_decode_mfma_kernel(const Att
                                          ((lane ^ swz_v(r)) * 16)) = new_v;
         }
       }
-      bool cur_ok = ok_slot[0];
-#pragma unroll
-      for (int j = 1; j < NS; ++j)
-        if (slot == j) cur_ok = ok_slot[j];
       compute(k, cur, cur_ok);
       if (k + NW >= ntiles) break;
       // The fragment reads of this slot have returned (compute used them);

@@ -212,6 +212,15 @@ __global__ __launch_bounds__(kThreads, 3) void paged_prefill_mfma_kernel(const A
     ld_k[i] = ((lane % 16) ^ swz_k(key)) * 8;  // logical chunk offsets (elements)
     ld_v[i] = ((lane % 16) ^ swz_v(key)) * 8;
   }
+  // Paged caches: byte offsets from the wave's half-tile base (row within
+  // the half, then chunk), constant over the whole loop, so a tile's loads
+  // take the scalar base form and need no per-lane address arithmetic.
+  uint32_t off_k[kRowsPerWave / 4], off_v[kRowsPerWave / 4];
+#pragma unroll
+  for (int i = 0; i < kRowsPerWave / 4; ++i) {
+    off_k[i] = static_cast<uint32_t>(((ld_key[i] % 16) * c_ts + ld_k[i]) * 2);
+    off_v[i] = static_cast<uint32_t>(((ld_key[i] % 16) * c_ts + ld_v[i]) * 2);
+  }
   // Issue the loads of `tile` into (kbuf, vbuf); returns the tile's mask
   // (bit h: its 16-key half h has a valid block id).
   auto issue_tile = [&](int tile, R* kbuf, R* vbuf) {
@@ -246,6 +255,17 @@ __global__ __launch_bounds__(kThreads, 3) void paged_prefill_mfma_kernel(const A
       } else {
         wbase = static_cast<int64_t>(wk ? wid : 0) * a.c_bs + row * a.c_ts + head_off;
       }
+      // Every row read lies in the half's block (ids are clamped to the
+      // request's last block; an invalid id reads block 0): keys past the
+      // range read that block's later rows, masked in the scores and zeroed
+      // in V before use.
+#pragma unroll
+      for (int i = 0; i < kRowsPerWave / 4; ++i) {
+        const int row0 = wave * kRowsPerWave + 4 * i;  // wave-uniform
+        lds_load16_sbase(kc + wbase, off_k[i], kbuf + row0 * kD);
+        lds_load16_sbase(vc + wbase, off_v[i], vbuf + row0 * kD);
+      }
+      return (ok[0] ? 1 : 0) | (ok[1] ? 2 : 0);
     } else {
       if constexpr (A32) {
         wbase = (static_cast<int>(krow0) + wt0) * c_ts + head_off32;
@@ -257,8 +277,8 @@ __global__ __launch_bounds__(kThreads, 3) void paged_prefill_mfma_kernel(const A
 #pragma unroll
     for (int i = 0; i < kRowsPerWave / 4; ++i) {
       const int row0 = wave * kRowsPerWave + 4 * i;  // wave-uniform
-      // Keys past the range or in a block with an invalid id read the head's
-      // first row instead (always in bounds; their scores are masked).
+      // Contiguous K/V: keys past the range read the head's first row
+      // instead (always in bounds; their scores are masked).
       const bool valid = wok && t0 + ld_key[i] < kv_end;
       const int64_t row = valid ? wbase + (ld_key[i] % 16) * c_ts : head_off;
       lds_load16(kc + row + ld_k[i], kbuf + row0 * kD);
@@ -392,7 +412,7 @@ __global__ __launch_bounds__(kThreads, 3) void paged_prefill_mfma_kernel(const A
   // tile t + 2 into the buffer tile t - 1 used, compute tile t.
   // The loop sits inside the prologue's branch so that every path into it
   // has passed the prologue (the compiler's wait insertion is static).
-  auto wait_tile = [&](bool next_in_flight) {
+  auto wait_tile = [&](bool next_in_flight, int tile, int tmask, R* vbuf) {
     // vmcnt(4) leaves the next tile's four loads in flight; vmcnt(0) waits
     // for everything (s_waitcnt encoding: vmcnt in bits 3:0, expcnt 6:4 = 7
     // (no wait), lgkmcnt 11:8).
@@ -404,9 +424,25 @@ __global__ __launch_bounds__(kThreads, 3) void paged_prefill_mfma_kernel(const A
     else
       __builtin_amdgcn_s_waitcnt(0x0070);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    // A tail tile (past kv_end) or a half with an invalid block id holds
+    // whatever the cache holds there: weight 0, but 0 * NaN is NaN, so each
+    // wave zeroes those of its own V rows before the barrier publishes the
+    // tile (K needs nothing: its scores are replaced by -inf).
+    const int t0 = tile * kKeys;
+    if (t0 + kKeys > kv_end || tmask != 3) {
+      const int row = wave * kRowsPerWave + lane / 8;
+      if (t0 + row >= kv_end || !((tmask >> (row / 16)) & 1)) {
+        R* dst = vbuf + row * kD + (lane % 8) * 16;
+        store_pack<R, 8>(dst, zero_pack<R, 8>());
+        store_pack<R, 8>(dst + 8, zero_pack<R, 8>());
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the zeros are in LDS
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    }
     __builtin_amdgcn_s_barrier();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
   };
+  static_assert(kRowsPerWave * kD * 2 == kWave * 32, "V-row zeroing: 32 bytes per lane");
   static_assert(kRowsPerWave / 4 * 2 == 4, "vmcnt above assumes four loads per wave per tile");
   if (ntiles > 0) {
     int mask[3] = {0, 0, 0};
@@ -421,9 +457,9 @@ __global__ __launch_bounds__(kThreads, 3) void paged_prefill_mfma_kernel(const A
     __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
     int cur = 0;
     for (int t = 0; t < ntiles; ++t) {
-      wait_tile(t + 1 < ntiles);
       const int nxt = cur == 0 ? 2 : cur - 1;  // (t + 2) % 3
       const int mcur = cur == 0 ? mask[0] : (cur == 1 ? mask[1] : mask[2]);
+      wait_tile(t + 1 < ntiles, t, mcur, s_v[cur]);
       if (t + 2 < ntiles) {
         const int m2 = issue_tile(t + 2, s_k[nxt], s_v[nxt]);
         if (nxt == 0) mask[0] = m2; else if (nxt == 1) mask[1] = m2; else mask[2] = m2;

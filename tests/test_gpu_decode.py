@@ -230,6 +230,43 @@ def test_poison_is_never_read_and_bad_table_entries_are_masked():
     assert torch.isfinite(out).all()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("split_k", [None, 1])
+def test_mfma_decode_never_uses_nan_slots(dtype, split_k):
+    """16 Q / 8 KV heads, head_dim 128, 16-bit caches: the MFMA kernel reads
+    whole 16-row tiles, so slots past each context (NaN here, as in an
+    uninitialised pool) reach the tile; their weights are 0 and their V rows
+    are zeroed before P.V, so the output matches the oracle, which like the
+    reference's masked loads never reads them."""
+    torch.manual_seed(6)
+    kc = torch.full((64, 16, 8, 128), float("nan"), device=DEV).to(dtype)
+    vc = kc.clone()
+    contexts = [20, 33, 1, 16, 100, 47]
+    tables = torch.full((len(contexts), 8), -1, dtype=torch.int32, device=DEV)
+    ids = torch.randperm(63, device=DEV)[:sum((c + 15) // 16 for c in contexts)] + 1
+    used = 0
+    for r, c in enumerate(contexts):
+        n = (c + 15) // 16
+        tables[r, :n] = ids[used:used + n].int()
+        used += n
+        for pos in range(c):
+            blk = int(tables[r, pos // 16])
+            kc[blk, pos % 16] = torch.randn(8, 128, device=DEV).to(dtype)
+            vc[blk, pos % 16] = torch.randn(8, 128, device=DEV).to(dtype)
+    q = torch.randn(len(contexts), 16, 128, device=DEV).to(dtype)
+    lens = torch.tensor(contexts, dtype=torch.int32, device=DEV)
+    out = hip_paged_decode(q, kc, vc, tables, lens, split_k=split_k)
+    assert torch.isfinite(out).all()
+    expected = oracle_decode(q, kc, vc, tables, lens, 1 / math.sqrt(128))
+    assert max_abs(out, expected) <= TOLERANCE[dtype]
+    # Invalid ids read block 0 (all NaN) and drop out of the softmax.
+    bad = tables.clone()
+    bad[4, 1] = -1
+    bad[5, 0] = 10 ** 6
+    out = hip_paged_decode(q, kc, vc, bad, lens, split_k=split_k)
+    assert torch.isfinite(out).all()
+
+
 def test_split_counters_are_left_zeroed():
     from microinfer_amd.layer import hip_paged_attention as ops
 

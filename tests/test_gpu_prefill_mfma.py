@@ -40,7 +40,8 @@ def _paged_case(q_lens, prefixes, hq, hkv, block_size, dtype, seed, poison=False
     for r, n in enumerate(nblk):
         tables[r, :n] = perm[used:used + n]
         used += n
-    fill = 1000.0 if poison else 0.0
+    # poison: True puts +-1000 in unused slots, a float puts that value.
+    fill = float(poison) if isinstance(poison, float) else (1000.0 if poison else 0.0)
     kc = torch.randn(pool, block_size, hkv, D, generator=gen)
     vc = torch.randn(pool, block_size, hkv, D, generator=gen)
     if poison:
@@ -100,6 +101,40 @@ def test_poison_in_unused_slots_is_never_read():
     assert torch.isfinite(out).all()
     expected = oracle_prefill(q, kc, vc, tables, contexts, cu_q, 1 / math.sqrt(D))
     assert max_abs(out, expected) <= 2e-2
+
+
+def test_nan_in_unused_slots_and_invalid_blocks_stays_out():
+    """Slots past each context and blocks no table names hold NaN, as an
+    uninitialised pool may: the reference's masked loads never read them
+    (microinfer/layer/triton_paged_attention.py:176-218), so the output must
+    stay finite and equal the oracle's. Tail tiles read those slots as whole
+    rows; their weights are 0 and their V rows are zeroed before use."""
+    q_lens = [17, 64, 1, 33, 5]
+    prefixes = [10, 100, 250, 0, 31]
+    q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, 16, 8, 16,
+                                                          torch.bfloat16, 5,
+                                                          poison=float("nan"))
+    assert not torch.isfinite(vc).all()
+    out = _run(q, kc, vc, tables, cu_q, cu_k)
+    assert torch.isfinite(out).all()
+    expected = oracle_prefill(q, kc, vc, tables, contexts, cu_q, 1 / math.sqrt(D))
+    assert max_abs(out, expected) <= 2e-2
+    # Invalid ids inside the contexts read block 0 instead, and drop out of
+    # the softmax; make block 0 an unused (NaN) block first.
+    named = set(int(b) for b in tables.flatten().tolist() if b >= 0)
+    spare = next(b for b in range(kc.shape[0]) if b not in named)
+    if 0 in named:
+        for cache in (kc, vc):
+            keep = cache[0].clone()
+            cache[0] = cache[spare]
+            cache[spare] = keep
+        tables = torch.where(tables == 0, torch.full_like(tables, spare), tables)
+    assert not torch.isfinite(vc[0]).any()
+    bad = tables.clone()
+    bad[1, 2] = -1
+    bad[3, 0] = 10 ** 6
+    out = _run(q, kc, vc, bad, cu_q, cu_k)
+    assert torch.isfinite(out).all()
 
 
 def test_invalid_table_entries_are_masked():
