@@ -1232,11 +1232,17 @@ def run_long_decode(args) -> int:
 
     from microinfer_amd.layer.hip_paged_attention import decode_plan, hip_paged_decode
 
+    from microinfer_amd.worker.kv_cache import KVCache
+
     dev = torch.device("cuda", 0)
     hq, hkv, d, bs, num_blocks = 32, 8, 128, 16, 65536
     gen = torch.Generator(device=dev).manual_seed(0)
-    kc = torch.randn((num_blocks, bs, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
-    vc = torch.randn((num_blocks, bs, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
+    # The product's cache (the --layout physical layout), logical [N, B, Hkv, D] views.
+    cache = KVCache(1, num_blocks, bs, hkv, d, dtype=torch.bfloat16, device=dev,
+                    layout=args.layout)
+    kc, vc = cache.keys[0], cache.values[0]
+    for pool in (kc, vc):
+        pool.copy_(torch.randn(pool.shape, generator=gen, device=dev))
     rng = np.random.default_rng(0)
     perm = torch.tensor(rng.permutation(num_blocks).astype(np.int32), device=dev)
     cases = {}
@@ -1284,6 +1290,7 @@ def run_long_decode(args) -> int:
                            "tokens, one launch (partitions merged in the launch)"),
               "cases_us": {k: round(v[0], 2) for k, v in cases.items()},
               "cases_gbs": {k: round(v[1] / v[0] / 1e3, 1) for k, v in cases.items()},
+              "kv_layout": args.layout,
               "note": "1 x 4096 (16.8 MB) is launch-latency-bound"}
     return _hbm_line("long-context paged decode HBM GB/s (% peak)", achieved, us, nbytes,
                      "paged_decode_mfma_kernel (split + in-launch merge)", args,
@@ -1299,7 +1306,8 @@ def main() -> int:
     parser.add_argument("--warmup-seconds", type=float, default=1.0,
                         help="keep running untimed warmup steps until this long has passed")
     parser.add_argument("--layers", type=int, default=28)
-    parser.add_argument("--layout", default="head_major", choices=["head_major", "token_major"])
+    parser.add_argument("--layout", default="paired",
+                        choices=["paired", "head_major", "token_major"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-engine", action="store_true",
                         help="decode: leave out the engine half of the line (decode tok/s of "

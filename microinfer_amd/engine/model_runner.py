@@ -23,7 +23,7 @@ from microinfer_amd.worker.kv_cache import KVCache
 
 class ModelRunner:
     def __init__(self, model, config: EngineConfig, *, num_blocks: int, block_size: int,
-                 layout: str = "head_major"):
+                 layout: str = "paired"):
         c = model.config
         self.model, self.config = model, config
         self.num_blocks, self.block_size = num_blocks, block_size

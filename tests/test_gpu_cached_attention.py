@@ -28,7 +28,7 @@ def dense_reference(q, k, v):
     return result.float()
 
 
-@pytest.mark.parametrize("layout", ["head_major", "token_major"])
+@pytest.mark.parametrize("layout", ["paired", "head_major", "token_major"])
 @pytest.mark.parametrize("checked", [True, False])
 def test_chunks_and_decode_match_full_prefill(layout, checked, seeded_torch):
     q, k, v = torch.randn(6, 4, 4), torch.randn(6, 2, 4), torch.randn(6, 2, 4)

@@ -60,7 +60,7 @@ def test_decode_matches_reference_small(block_size, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("layout", ["head_major", "token_major"])
+@pytest.mark.parametrize("layout", ["paired", "head_major", "token_major"])
 def test_small_decode_workload_append_then_attend(dtype, layout):
     # 0.6B layer, pool 1024, 8 sequences, contexts U[64, 512], seed 0: the
     # append writes position c-1, then attention reads all c tokens.
@@ -84,7 +84,7 @@ def test_small_decode_workload_append_then_attend(dtype, layout):
     assert max_abs(out, expected) <= TOLERANCE[dtype]
 
 
-@pytest.mark.parametrize("layout", ["head_major", "token_major"])
+@pytest.mark.parametrize("layout", ["paired", "head_major", "token_major"])
 def test_decode_batch32_workload(layout):
     # 0.6B shape, bf16, pool 16384, 32 sequences, contexts U[128, 2048].
     batch = make_decode_batch(num_seqs=32, ctx_lo=128, ctx_hi=2048, pool_blocks=16384,

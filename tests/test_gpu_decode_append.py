@@ -30,7 +30,7 @@ def decode_slots(tables: np.ndarray, contexts, block_size: int) -> np.ndarray:
 
 
 @pytest.mark.parametrize("split_k", [None, 1, 4, 64])
-@pytest.mark.parametrize("layout", ["head_major", "token_major"])
+@pytest.mark.parametrize("layout", ["paired", "head_major", "token_major"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_fused_append_matches_append_then_attend(dtype, layout, split_k):
     batch = make_decode_batch(num_seqs=8, ctx_lo=1, ctx_hi=700, pool_blocks=1024, **QWEN3_06B)

@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-@pytest.mark.parametrize("layout", ["head_major", "token_major"])
+@pytest.mark.parametrize("layout", ["paired", "head_major", "token_major"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_gather_small_bit_exact(layout, dtype):
     torch.manual_seed(0)

@@ -29,7 +29,7 @@ def filled_cache(batch, dtype, layout):
     return cache
 
 
-@pytest.mark.parametrize("layout", ["head_major", "token_major"])
+@pytest.mark.parametrize("layout", ["paired", "head_major", "token_major"])
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("slot_dtype", [torch.int32, torch.int64])
 def test_append_small_decode_workload_bit_exact(layout, dtype, slot_dtype):
@@ -46,7 +46,7 @@ def test_append_small_decode_workload_bit_exact(layout, dtype, slot_dtype):
     assert np.array_equal(bits(view.values), expected_v)
 
 
-@pytest.mark.parametrize("layout", ["head_major", "token_major"])
+@pytest.mark.parametrize("layout", ["paired", "head_major", "token_major"])
 def test_append_full_decode_pool(layout):
     # 0.6B shape, bf16, pool 16384, 32 sequences, contexts U[128, 2048].
     batch = make_decode_batch(num_seqs=32, ctx_lo=128, ctx_hi=2048, pool_blocks=16384,

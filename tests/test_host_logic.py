@@ -58,7 +58,7 @@ def test_slot_indices_are_cached_per_block_size():
     assert blocks2.tolist() == [0, 2, 1] and offsets2.tolist() == [0, 1, 0]
 
 
-@pytest.mark.parametrize("layout", ["head_major", "token_major"])
+@pytest.mark.parametrize("layout", ["paired", "head_major", "token_major"])
 def test_cache_layout_byte_budget_and_views(layout):
     cache = KVCache(2, 3, 4, 2, 3, layout=layout)
     assert cache.keys.shape == cache.values.shape == (2, 3, 4, 2, 3)
@@ -66,7 +66,15 @@ def test_cache_layout_byte_budget_and_views(layout):
     view = cache.layer(1)
     assert view.keys.untyped_storage().data_ptr() == cache.keys.untyped_storage().data_ptr()
     assert view.block_size == 4
-    if layout == "head_major":
+    if layout == "paired":
+        # K then V of one KV head's block are one contiguous run: token
+        # stride D, head stride 2*B*D, V one B*D after K, equal strides.
+        assert view.keys.stride() == view.values.stride() == (2 * 2 * 4 * 3, 3, 2 * 4 * 3, 1)
+        assert view.values.data_ptr() - view.keys.data_ptr() == 4 * 3 * 4
+        cache.values[1, 2, 3, 1] = -5.0
+        assert cache.keys[1, 2, 3, 1].eq(0).all()
+        cache.values[1, 2, 3, 1] = 0.0
+    elif layout == "head_major":
         # One KV head's block is contiguous: token stride D, head stride B*D.
         assert view.keys.stride() == (2 * 4 * 3, 3, 4 * 3, 1)
     else:
