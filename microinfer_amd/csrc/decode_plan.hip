@@ -6,9 +6,13 @@
 // (microinfer/layer/triton_paged_attention.py:342-349) and stripes tiles over
 // the splits (:76-79). Here partitions are contiguous block ranges sized from
 // the step's total context: about kTargetItems (item, KV head) workgroups of
-// at least kMinPartBlocks blocks each. Sequences are ordered longest first,
-// so the partitions of split sequences run (and merge) early while shorter
-// single-partition items keep the memory system busy at the end.
+// at least kMinPartBlocks blocks each. A sequence's partitions occupy
+// consecutive slots (first_item + part: where their partials go), but the
+// launch dispatches items largest first, whatever their sequence: the
+// hardware does not start a later workgroup on a CU that an early small item
+// freed until well into the launch, so a small item in the first round
+// leaves its CU idle, while small items at the end of the grid fill the
+// tail.
 #include "paged_attention.h"
 
 namespace mi {
@@ -41,6 +45,8 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
   __shared__ int s_order[kMaxPlanSeqs];  // rank -> sequence
   __shared__ int s_first[kMaxPlanSeqs];  // rank -> first item index
   __shared__ int s_scan[kPlanThreads];
+  __shared__ int s_size[kSortLimit];  // slot -> blocks (size-ordered dispatch)
+  __shared__ int s_rank[kSortLimit];  // slot -> plan position
   __shared__ int s_total_blocks;
   __shared__ int s_total_items;
   const int tid = threadIdx.x;
@@ -115,7 +121,35 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
   if (tid == kPlanThreads - 1) s_total_items = s_scan[tid];
   __syncthreads();
 
-  // Emit the items, then mark the rest of the launch's slots unused.
+  // Emit the items, then mark the rest of the launch's slots unused. Slots
+  // (first_item + part) number a sequence's partitions consecutively; the
+  // plan position a workgroup reads is the item's rank by size, largest
+  // first (ties in slot order), so every workgroup of the first round is
+  // one of the largest and the launch ends with the smallest items.
+  const int total_items = min(s_total_items, max_items);
+  const bool by_size = total_items <= kSortLimit;
+  if (by_size) {
+    for (int k = tid; k < num_seqs; k += kPlanThreads) {
+      const int nb = blocks_of(s_ctx[s_order[k]], block_size, lb);
+      const int pb = part_blocks(nb, split_k, pb_global);
+      const int np = max(1, (nb + pb - 1) / pb);
+      for (int p = 0; p < np && s_first[k] + p < max_items; ++p)
+        s_size[s_first[k] + p] = min(nb, (p + 1) * pb) - p * pb;
+    }
+    __syncthreads();
+    // One thread per slot: its rank among all items (every thread reads the
+    // same size at a time, an LDS broadcast).
+    for (int i = tid; i < total_items; i += kPlanThreads) {
+      const int sz = s_size[i];
+      int r = 0;
+      for (int j = 0; j < total_items; ++j) {
+        const int o = s_size[j];
+        r += (o > sz) || (o == sz && j < i);
+      }
+      s_rank[i] = r;
+    }
+    __syncthreads();
+  }
   for (int k = tid; k < num_seqs; k += kPlanThreads) {
     const int r = s_order[k];
     const int c = s_ctx[r];
@@ -133,7 +167,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
       it.ctx = c;
       it.part = p;
       it.unused = 0;
-      plan[f + p] = it;
+      plan[by_size ? s_rank[f + p] : f + p] = it;
     }
   }
   for (int i = s_total_items + tid; i < max_items; i += kPlanThreads) {

@@ -57,7 +57,7 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
   const int w = blockIdx.x / a.num_kv_heads;
   const int G = EXACT ? GMAX : a.group;
 
-  int seq, q_row, ctx, blk_begin, blk_end, nparts, first_item = 0;
+  int seq, q_row, ctx, blk_begin, blk_end, nparts, first_item = 0, part = 0;
   if (a.varlen) {
     q_row = w;
     int lo = 0, hi = a.num_seqs - 1;
@@ -92,6 +92,7 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
     blk_end = min(it.blk_end, a.t_width);
     nparts = it.nparts;
     first_item = it.first_item;
+    part = it.part;
   }
 
   // Fused append (decode): the partition holding position ctx - 1 owns the
@@ -391,9 +392,11 @@ __global__ __launch_bounds__(kWave * NW, 2) void paged_attention_vector_kernel(c
 
   // Publish this partition's state, then count arrivals; the last workgroup
   // of the (sequence, KV head) merges every partition and writes the output.
-  // Partials of item w: ws_acc[(w*Hkv + head)*G + g][D], ws_ml[...][2].
+  // Partials in the partition's slot (first_item + part; the plan may
+  // dispatch items in any order): ws_acc[(slot*Hkv + head)*G + g][D],
+  // ws_ml[...][2].
   {
-    const int64_t base = (static_cast<int64_t>(w) * a.num_kv_heads + head) * G;
+    const int64_t base = (static_cast<int64_t>(first_item + part) * a.num_kv_heads + head) * G;
 #pragma unroll
     for (int g = 0; g < GMAX; ++g) {
       if (!EXACT && g >= G) continue;

@@ -433,8 +433,10 @@ __global__ __launch_bounds__(kWave * NW) void paged_decode_mfma_kernel(const Att
     return;
   }
 
-  // Publish this partition: ws_acc[(w Hkv + head) G + h][d], ws_ml[...][2].
-  const int64_t base = (static_cast<int64_t>(w) * a.num_kv_heads + head) * G;
+  // Publish this partition in its slot (first_item + part; the plan may
+  // dispatch items in any order): ws_acc[(slot Hkv + head) G + h][d],
+  // ws_ml[...][2].
+  const int64_t base = (static_cast<int64_t>(it.first_item + it.part) * a.num_kv_heads + head) * G;
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int e = tid + j * kThreads;
