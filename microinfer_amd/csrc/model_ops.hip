@@ -51,12 +51,18 @@ struct LinArgs {
   void* y;
   int64_t ys;
   int32_t m, n, k;
+  int32_t row_tiles;  // RT launches: 16-row tiles of x, one per workgroup
 };
 
 // NW waves split k (wave w: a contiguous range of k-steps); NT 16-column
 // tiles per workgroup; MT 16-row tiles of x (m <= 16 MT). The waves' float32
 // sums meet in LDS and are added in wave order.
-template <typename E, int NW, int NT, int MT>
+// RT: each workgroup takes one 16-row tile of x (MT = 1) instead of every
+// row, so x is read once per column tile rather than once per row tile and
+// column tile; the row tiles of a column tile get blockIdx values equal
+// modulo 8 -- the same XCD, so they share its L2 -- and are dispatched
+// together, so the weights still come from HBM about once.
+template <typename E, int NW, int NT, int MT, bool RT>
 __global__ __launch_bounds__(NW * kWave) void linear_kernel(const LinArgs a) {
   using M = LinMfma<E>;
   using vec8 = typename M::vec8;
@@ -68,7 +74,14 @@ __global__ __launch_bounds__(NW * kWave) void linear_kernel(const LinArgs a) {
   const int wave = tid / kWave;
   const int col = lane % 16;   // weight row (output column) / x row within a tile
   const int quad = lane / 16;  // 8-element group of the k-step
-  const int n0 = blockIdx.x * (16 * NT);
+  static_assert(!RT || MT == 1, "row-tiled launches take one row tile");
+  int n0 = blockIdx.x * (16 * NT), r0 = 0;
+  if constexpr (RT) {
+    const int xcd = blockIdx.x % 8;
+    const int rest = blockIdx.x / 8;
+    r0 = 16 * (rest % a.row_tiles);
+    n0 = ((rest / a.row_tiles) * 8 + xcd) * (16 * NT);
+  }
   const int total = a.k / kLinStep;
   const int per_wave = (total + NW - 1) / NW;
   const int s_begin = wave * per_wave;
@@ -92,7 +105,7 @@ __global__ __launch_bounds__(NW * kWave) void linear_kernel(const LinArgs a) {
   bool xok[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
-    const int r = 16 * t + col;
+    const int r = r0 + 16 * t + col;
     xok[t] = r < a.m;
     xrow[t] = static_cast<const R*>(a.x) + static_cast<int64_t>(xok[t] ? r : 0) * a.xs + quad * 8;
   }
@@ -155,7 +168,7 @@ __global__ __launch_bounds__(NW * kWave) void linear_kernel(const LinArgs a) {
     if (!wok[u]) continue;
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      const int r = 16 * t + col;
+      const int r = r0 + 16 * t + col;
       if (r < a.m) {
         Pack<R, 4> v;
 #pragma unroll
@@ -167,31 +180,55 @@ __global__ __launch_bounds__(NW * kWave) void linear_kernel(const LinArgs a) {
 }
 
 template <typename E, int NW, int NT>
-void launch_linear_mt(const LinArgs& a, hipStream_t stream) {
-  const dim3 grid(static_cast<uint32_t>((a.n + 16 * NT - 1) / (16 * NT)));
-  switch ((a.m + 15) / 16) {
-    case 1: linear_kernel<E, NW, NT, 1><<<grid, NW * kWave, 0, stream>>>(a); break;
-    case 2: linear_kernel<E, NW, NT, 2><<<grid, NW * kWave, 0, stream>>>(a); break;
-    case 3: linear_kernel<E, NW, NT, 3><<<grid, NW * kWave, 0, stream>>>(a); break;
-    default: linear_kernel<E, NW, NT, 4><<<grid, NW * kWave, 0, stream>>>(a); break;
+void launch_linear_mt(LinArgs a, bool row_tiled, hipStream_t stream) {
+  const int col_tiles = (a.n + 16 * NT - 1) / (16 * NT);
+  const int row_tiles = (a.m + 15) / 16;
+  if (row_tiled && row_tiles > 1) {
+    a.row_tiles = row_tiles;
+    const dim3 grid(static_cast<uint32_t>((col_tiles + 7) / 8 * 8 * row_tiles));
+    linear_kernel<E, NW, NT, 1, true><<<grid, NW * kWave, 0, stream>>>(a);
+    return;
+  }
+  const dim3 grid(static_cast<uint32_t>(col_tiles));
+  switch (row_tiles) {
+    case 1: linear_kernel<E, NW, NT, 1, false><<<grid, NW * kWave, 0, stream>>>(a); break;
+    case 2: linear_kernel<E, NW, NT, 2, false><<<grid, NW * kWave, 0, stream>>>(a); break;
+    case 3: linear_kernel<E, NW, NT, 3, false><<<grid, NW * kWave, 0, stream>>>(a); break;
+    default: linear_kernel<E, NW, NT, 4, false><<<grid, NW * kWave, 0, stream>>>(a); break;
   }
 }
 
-// Workgroup shape: 16 columns per workgroup while that gives at most a few
-// workgroups per CU, else 32 (each x fragment then serves two weight tiles,
-// halving the x traffic of very wide products such as the vocabulary
-// projection); eight waves split k when the columns give fewer workgroups
-// than CUs, so each CU keeps more weight loads in flight.
+// Workgroup shape, from hipGraph-replayed timings of the Qwen3-0.6B
+// projections on MI355X (us per launch at 64 rows):
+//  * up to 16 rows (one row tile): 16 columns per workgroup while that gives
+//    at most a few workgroups per CU, else 32 (each x fragment then serves
+//    two weight tiles); eight waves split k when the columns give fewer
+//    workgroups than CUs;
+//  * more rows, n <= 2048: row-tiled, 8 waves, 16 columns (output projection
+//    6.1 against 11.9 with every row per workgroup; down projection 8.1
+//    against 16.3);
+//  * more rows, n <= 4096: row-tiled, 8 waves, 32 columns (QKV 8.1 against
+//    8.6);
+//  * more rows, wider: every row per workgroup, 4 waves, 32 columns (gate/up
+//    10.4 against 12.0 row-tiled).
 template <typename E>
 int32_t launch_linear(const LinArgs& a, hipStream_t stream) {
   const int cus = device_cus();
   const int64_t tiles16 = a.n / 16;
-  if (tiles16 >= 8 * static_cast<int64_t>(cus))
-    launch_linear_mt<E, 4, 2>(a, stream);
-  else if (tiles16 >= cus)
-    launch_linear_mt<E, 4, 1>(a, stream);
-  else
-    launch_linear_mt<E, 8, 1>(a, stream);
+  if (a.m <= 16) {
+    if (tiles16 >= 8 * static_cast<int64_t>(cus))
+      launch_linear_mt<E, 4, 2>(a, false, stream);
+    else if (tiles16 >= cus)
+      launch_linear_mt<E, 4, 1>(a, false, stream);
+    else
+      launch_linear_mt<E, 8, 1>(a, false, stream);
+  } else if (a.n <= 2048) {
+    launch_linear_mt<E, 8, 1>(a, true, stream);
+  } else if (a.n <= 4096) {
+    launch_linear_mt<E, 8, 2>(a, true, stream);
+  } else {
+    launch_linear_mt<E, 4, 2>(a, false, stream);
+  }
   return check_launch("mi_linear");
 }
 

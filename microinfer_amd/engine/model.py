@@ -14,9 +14,10 @@ On this path the per-layer Q/K norm + RoPE + KV append is one HIP launch
 prefill (``paged_attention_meta`` / ``varlen_attention``), and RMSNorm with
 its residual sum and the SwiGLU gate are HIP launches too (``hip_dense``:
 the counterparts of the reference's compiled ``_compiled_add_rms_norm`` /
-``_compiled_swiglu``), as are the projections of small decode batches where
-the HIP product is measured faster than torch's (``prefer_hip_linear``); the
-rest stay on torch (hipBLASLt). Weights are random:
+``_compiled_swiglu``), as are the projections of decode batches (up to 64
+rows) where the HIP product is measured faster than torch's
+(``prefer_hip_linear``); the rest stay on torch (hipBLASLt). Weights are
+random:
 N(0, 0.02) from a seeded generator, norm weights 1, since no checkpoint is
 available to load (``init_std`` sets the spread).
 """

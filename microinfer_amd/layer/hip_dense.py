@@ -8,7 +8,9 @@ microinfer/layer/transformer.py:12-15, ``FFN.forward`` :82-88) and every
 projection as ``F.linear``. Each function here is one HIP launch with the
 same result up to float32 summation order; ``supported_*`` tell the caller
 when a request is outside what the kernels take (32-bit tensors, more than
-64 rows for a projection, unaligned rows), so the caller keeps torch for it.
+64 rows for a projection, unaligned rows) and ``prefer_hip_linear`` when the
+HIP projection is measured faster than torch's, so the caller keeps torch for
+the rest.
 """
 
 from __future__ import annotations
@@ -37,16 +39,14 @@ def supported_linear(x: torch.Tensor, weight: torch.Tensor) -> bool:
 def prefer_hip_linear(x: torch.Tensor, weight: torch.Tensor) -> bool:
     """Whether ``hip_linear`` beats torch's product for this request.
 
-    Measured on MI355X (hipGraph-replayed, the Qwen3-0.6B projections): the
-    HIP product wins at up to 16 rows (QKV 4.1 against 5.9 us at 8 rows, down
-    projection 7.0 against 9.1) and at up to 32 rows when k <= 2048; past
-    that every 16-column workgroup re-reads all of x in 16-row x 64-byte
-    pieces and hipBLASLt is faster (64 rows: down projection 16.3 against
-    9.7 us)."""
+    Measured on MI355X (hipGraph-replayed, the Qwen3-0.6B projections, us per
+    launch, HIP against hipBLASLt): at 64 rows QKV 8.1 / 8.5, output 6.1 /
+    8.0, gate/up 10.4 / 11.9, down 8.1 / 9.7; at 8 rows 4.1 / 5.9, 5.3 /
+    8.1, 6.2 / 8.0, 7.0 / 9.1. The vocabulary projection (151936 columns)
+    stays on hipBLASLt past 16 rows (64 rows: 138 against 85)."""
     if not supported_linear(x, weight):
         return False
-    m, k = x.shape
-    return m <= 16 or (m <= 32 and k <= 2048)
+    return x.shape[0] <= 16 or weight.shape[0] <= 32768
 
 
 def hip_linear(x: torch.Tensor, weight: torch.Tensor, *,
