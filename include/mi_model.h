@@ -40,6 +40,20 @@ int32_t mi_linear(const void* x, int64_t x_row_stride, const void* w, int64_t w_
                   int32_t dtype, void* stream);
 
 /*
+ * The FFN's gate/up projection with its SwiGLU gate (FFN.forward,
+ * microinfer/layer/transformer.py:82-88: gate_up = F.linear(x, w), then
+ * _compiled_swiglu :12-15): w holds 2 * inter rows, the gate's then the up
+ * projection's; y[m, inter] = round(round(silu(g)) * u) with
+ * g = round(x . w[c]^T), u = round(x . w[inter + c]^T) -- mi_linear followed
+ * by mi_silu_mul, bit for bit, in one launch that writes only y.
+ * inter % 16 == 0, k % 32 == 0, every pointer and row stride 16-byte
+ * aligned; m > 64 returns MI_ERR_UNSUPPORTED.
+ */
+int32_t mi_linear_swiglu(const void* x, int64_t x_row_stride, const void* w,
+                         int64_t w_row_stride, void* y, int64_t y_row_stride, int32_t m,
+                         int32_t inter, int32_t k, int32_t dtype, void* stream);
+
+/*
  * FuseLayerNorm's forward (microinfer/layer/norm.py:26-35) on `rows` rows:
  * s = x + residual (rounded to the element type; s = x when residual is
  * NULL), residual_out = s (skipped when residual_out is NULL), and

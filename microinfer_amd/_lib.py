@@ -79,6 +79,7 @@ SIGNATURES = {
          _P],
     ),
     "mi_linear": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I32, _I32, _I32, _I32, _P]),
+    "mi_linear_swiglu": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I32, _I32, _I32, _I32, _P]),
     "mi_rms_norm_residual": (
         _I32, [_P, _I64, _P, _I64, _P, _F32, _P, _I64, _P, _I64, _I32, _I32, _I32, _P]),
     "mi_silu_mul": (_I32, [_P, _I64, _P, _I64, _I32, _I32, _I32, _P]),

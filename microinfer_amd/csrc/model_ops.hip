@@ -12,6 +12,8 @@
 //  * mi_rms_norm_residual: one wave per row, the row held in registers
 //    between the sum of squares and the scaling.
 //  * mi_silu_mul: one 16-byte vector of gate and of up per thread.
+//  * mi_linear_swiglu: the gate/up projection with the SwiGLU gate in its
+//    epilogue (each workgroup sums a gate and the matching up tile).
 #include "mi_common.h"
 #include "mi_model.h"
 
@@ -39,6 +41,15 @@ struct LinMfma<F16> {
   }
 };
 
+// round(round(silu(g)) * u) on 16-bit inputs: the rounding steps of torch's
+// F.silu(gate) * up.
+template <typename E>
+__device__ __forceinline__ uint16_t silu_mul_round(uint16_t g, uint16_t u) {
+  const float x = E::load(g);
+  const float act = E::load(E::store(x / (1.f + expf(-x))));
+  return E::store(act * E::load(u));
+}
+
 constexpr int kLinStep = 32;   // k per MFMA
 constexpr int kLinChunk = 8;   // k-steps whose loads are issued together
 constexpr int kLinMaxRows = 64;
@@ -52,6 +63,7 @@ struct LinArgs {
   int64_t ys;
   int32_t m, n, k;
   int32_t row_tiles;  // RT launches: 16-row tiles of x, one per workgroup
+  int32_t inter;      // GLU launches: rows [0, inter) of w are the gate, the rest up
 };
 
 // NW waves split k (wave w: a contiguous range of k-steps); NT 16-column
@@ -62,7 +74,12 @@ struct LinArgs {
 // column tile; the row tiles of a column tile get blockIdx values equal
 // modulo 8 -- the same XCD, so they share its L2 -- and are dispatched
 // together, so the weights still come from HBM about once.
-template <typename E, int NW, int NT, int MT, bool RT>
+// GLU: the SwiGLU gate of a gate/up projection in the epilogue. Tile 0 is
+// gate columns n0 .. n0 + 15 (weight rows n0 + c), tile 1 the matching up
+// columns (weight rows inter + n0 + c); the workgroup writes
+// round(round(silu(gate)) * up) to columns n0 .. n0 + 15 of y, with gate and
+// up first rounded to the element type as the plain projection stores them.
+template <typename E, int NW, int NT, int MT, bool RT, bool GLU = false>
 __global__ __launch_bounds__(NW * kWave) void linear_kernel(const LinArgs a) {
   using M = LinMfma<E>;
   using vec8 = typename M::vec8;
@@ -75,7 +92,8 @@ __global__ __launch_bounds__(NW * kWave) void linear_kernel(const LinArgs a) {
   const int col = lane % 16;   // weight row (output column) / x row within a tile
   const int quad = lane / 16;  // 8-element group of the k-step
   static_assert(!RT || MT == 1, "row-tiled launches take one row tile");
-  int n0 = blockIdx.x * (16 * NT), r0 = 0;
+  static_assert(!GLU || (NT == 2 && !RT), "GLU launches: gate and up tiles, every row");
+  int n0 = blockIdx.x * (GLU ? 16 : 16 * NT), r0 = 0;
   if constexpr (RT) {
     const int xcd = blockIdx.x % 8;
     const int rest = blockIdx.x / 8;
@@ -97,9 +115,11 @@ __global__ __launch_bounds__(NW * kWave) void linear_kernel(const LinArgs a) {
   bool wok[NT];
 #pragma unroll
   for (int u = 0; u < NT; ++u) {
-    wok[u] = n0 + 16 * u < a.n;  // n % 16 == 0: a tile's columns exist or none do
+    // n % 16 == 0: a tile's columns exist or none do.
+    const int wr = GLU ? u * a.inter + n0 : n0 + 16 * u;
+    wok[u] = GLU ? n0 < a.inter : wr < a.n;
     wrow[u] = static_cast<const R*>(a.w) +
-              static_cast<int64_t>(wok[u] ? n0 + 16 * u + col : 0) * a.ws + quad * 8;
+              static_cast<int64_t>(wok[u] ? wr + col : 0) * a.ws + quad * 8;
   }
   const R* xrow[MT];
   bool xok[MT];
@@ -110,35 +130,34 @@ __global__ __launch_bounds__(NW * kWave) void linear_kernel(const LinArgs a) {
     xrow[t] = static_cast<const R*>(a.x) + static_cast<int64_t>(xok[t] ? r : 0) * a.xs + quad * 8;
   }
   for (int s0 = s_begin; s0 < s_end; s0 += kLinChunk) {
+    // Steps past the wave's range (a partial last chunk) get zero fragments
+    // and still run their MFMAs, adding 0: no MFMA sits under a per-step
+    // branch or exec mask (MFMA ignores EXEC).
     vec8 wf[kLinChunk][NT];
     vec8 xf[kLinChunk][MT];
 #pragma unroll
     for (int j = 0; j < kLinChunk; ++j) {
-      if (s0 + j < s_end) {
-        const int off = (s0 + j) * kLinStep;
+      const bool step_ok = s0 + j < s_end;
+      const int off = (s0 + j) * kLinStep;
 #pragma unroll
-        for (int u = 0; u < NT; ++u) {
-          Pack<R, 8> p = zero_pack<R, 8>();
-          if (wok[u]) p = load_pack<R, 8>(wrow[u] + off);
-          wf[j][u] = __builtin_bit_cast(vec8, p);
-        }
+      for (int u = 0; u < NT; ++u) {
+        Pack<R, 8> p = zero_pack<R, 8>();
+        if (step_ok && wok[u]) p = load_pack<R, 8>(wrow[u] + off);
+        wf[j][u] = __builtin_bit_cast(vec8, p);
+      }
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          Pack<R, 8> p = zero_pack<R, 8>();
-          if (xok[t]) p = load_pack<R, 8>(xrow[t] + off);
-          xf[j][t] = __builtin_bit_cast(vec8, p);
-        }
+      for (int t = 0; t < MT; ++t) {
+        Pack<R, 8> p = zero_pack<R, 8>();
+        if (step_ok && xok[t]) p = load_pack<R, 8>(xrow[t] + off);
+        xf[j][t] = __builtin_bit_cast(vec8, p);
       }
     }
 #pragma unroll
-    for (int j = 0; j < kLinChunk; ++j) {
-      if (s0 + j < s_end) {
+    for (int j = 0; j < kLinChunk; ++j)
 #pragma unroll
-        for (int u = 0; u < NT; ++u)
+      for (int u = 0; u < NT; ++u)
 #pragma unroll
-          for (int t = 0; t < MT; ++t) acc[u][t] = M::mma(wf[j][u], xf[j][t], acc[u][t]);
-      }
-    }
+        for (int t = 0; t < MT; ++t) acc[u][t] = M::mma(wf[j][u], xf[j][t], acc[u][t]);
   }
 
   // acc[u][t][j] = y^T[n0 + 16 u + 4 quad + j][16 t + col]. Every wave but
@@ -163,6 +182,20 @@ __global__ __launch_bounds__(NW * kWave) void linear_kernel(const LinArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[u][t][j] += s_acc[wv][(u * MT + t) * 4 + j][lane];
   R* y = static_cast<R*>(a.y);
+  if constexpr (GLU) {
+    if (!wok[0]) return;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int r = r0 + 16 * t + col;
+      if (r < a.m) {
+        Pack<R, 4> v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v.v[j] = silu_mul_round<E>(E::store(acc[0][t][j]), E::store(acc[1][t][j]));
+        store_pack<R, 4>(y + static_cast<int64_t>(r) * a.ys + n0 + 4 * quad, v);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int u = 0; u < NT; ++u) {
     if (!wok[u]) continue;
@@ -230,6 +263,21 @@ int32_t launch_linear(const LinArgs& a, hipStream_t stream) {
     launch_linear_mt<E, 4, 2>(a, false, stream);
   }
   return check_launch("mi_linear");
+}
+
+// Gate/up projection with the SwiGLU gate: 4 waves (as the plain projection
+// of that width, so gate and up are summed in the same order) over every row,
+// one gate and one up tile per workgroup.
+template <typename E>
+int32_t launch_linear_glu(LinArgs a, hipStream_t stream) {
+  const dim3 grid(static_cast<uint32_t>(a.inter / 16));
+  switch ((a.m + 15) / 16) {
+    case 1: linear_kernel<E, 4, 2, 1, false, true><<<grid, 4 * kWave, 0, stream>>>(a); break;
+    case 2: linear_kernel<E, 4, 2, 2, false, true><<<grid, 4 * kWave, 0, stream>>>(a); break;
+    case 3: linear_kernel<E, 4, 2, 3, false, true><<<grid, 4 * kWave, 0, stream>>>(a); break;
+    default: linear_kernel<E, 4, 2, 4, false, true><<<grid, 4 * kWave, 0, stream>>>(a); break;
+  }
+  return check_launch("mi_linear_swiglu");
 }
 
 // ---------------------------------------------------------------------------
@@ -345,11 +393,7 @@ __global__ __launch_bounds__(kSiluThreads) void silu_mul_kernel(const uint16_t* 
   const Pack<R, 8> u = load_pack<R, 8>(gu + r * gs + inter + c);
   Pack<R, 8> o;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float x = E::load(g.v[j]);
-    const float act = E::load(E::store(x / (1.f + expf(-x))));
-    o.v[j] = E::store(act * E::load(u.v[j]));
-  }
+  for (int j = 0; j < 8; ++j) o.v[j] = silu_mul_round<E>(g.v[j], u.v[j]);
   store_pack<R, 8>(out + r * os + c, o);
 }
 
@@ -467,4 +511,39 @@ extern "C" int32_t mi_silu_mul(const void* gate_up, int64_t gate_up_row_stride, 
     silu_mul_kernel<F16><<<static_cast<uint32_t>(blocks), kSiluThreads, 0, s>>>(
         gu, gate_up_row_stride, o, out_row_stride, rows, inter);
   return check_launch("mi_silu_mul");
+}
+
+extern "C" int32_t mi_linear_swiglu(const void* x, int64_t x_row_stride, const void* w,
+                                    int64_t w_row_stride, void* y, int64_t y_row_stride,
+                                    int32_t m, int32_t inter, int32_t k, int32_t dtype,
+                                    void* stream) {
+  using namespace mi;
+  clear_error();
+  if (!valid_dtype(dtype)) return fail(MI_ERR_INVALID_ARGUMENT, "mi_linear_swiglu: bad dtype");
+  if (m < 0 || inter <= 0 || k <= 0 || inter % 16 || k % kLinStep)
+    return fail(MI_ERR_INVALID_ARGUMENT,
+                "mi_linear_swiglu: need m >= 0, inter a positive multiple of 16, k of 32");
+  if (!half_type(dtype)) return fail(MI_ERR_UNSUPPORTED, "mi_linear_swiglu: 16-bit types only");
+  if (m > kLinMaxRows) return fail(MI_ERR_UNSUPPORTED, "mi_linear_swiglu: m above 64");
+  if (m == 0) return MI_OK;
+  if (!x || !w || !y) return fail(MI_ERR_INVALID_ARGUMENT, "mi_linear_swiglu: null pointer");
+  if (x_row_stride < k || w_row_stride < k || y_row_stride < inter)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_linear_swiglu: row strides below the row lengths");
+  if (!aligned16(x) || !aligned16(w) || !aligned16(y) || x_row_stride % 8 ||
+      w_row_stride % 8 || y_row_stride % 8)
+    return fail(MI_ERR_INVALID_ARGUMENT,
+                "mi_linear_swiglu: pointers and row strides must be 16-byte aligned");
+  LinArgs a{};
+  a.x = x;
+  a.xs = x_row_stride;
+  a.w = w;
+  a.ws = w_row_stride;
+  a.y = y;
+  a.ys = y_row_stride;
+  a.m = m;
+  a.n = 2 * inter;
+  a.k = k;
+  a.inter = inter;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dtype == MI_DTYPE_BF16 ? launch_linear_glu<BF16>(a, s) : launch_linear_glu<F16>(a, s);
 }

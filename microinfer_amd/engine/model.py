@@ -29,8 +29,8 @@ from dataclasses import dataclass
 import torch
 from torch.nn import functional as F
 
-from microinfer_amd.layer.hip_dense import (hip_linear, hip_rms_norm_residual, hip_silu_mul,
-                                            prefer_hip_linear, supported_rows)
+from microinfer_amd.layer.hip_dense import (hip_linear, hip_linear_swiglu, hip_rms_norm_residual,
+                                            hip_silu_mul, prefer_hip_linear, supported_rows)
 from microinfer_amd.layer.hip_qk_norm_rope import qk_norm_rope_append, rope_tables
 from microinfer_amd.layer.paged_attention import paged_attention_meta, varlen_attention
 
@@ -121,6 +121,13 @@ class Qwen3Model:
         gate, up = gate_up.chunk(2, dim=-1)
         return F.silu(gate) * up
 
+    def _ffn_gate(self, x, gate_up):
+        """SwiGLU of the gate/up projection: one fused launch where the HIP
+        projection is preferred, else the projection and then the gate."""
+        if self.hip_dense and prefer_hip_linear(x, gate_up) and gate_up.shape[0] % 32 == 0:
+            return hip_linear_swiglu(x, gate_up)
+        return self._swiglu(self._linear(x, gate_up))
+
     def forward(self, input_ids, positions, metadata):
         """Hidden states ``[T, H]`` of the packed tokens of one step."""
         c = self.config
@@ -147,7 +154,7 @@ class Qwen3Model:
                 attn = paged_attention_meta(rotated, cache.keys, cache.values, metadata)
             hidden = self._linear(attn.reshape(tokens, q_width), layer.out)
             x, residual = self._norm(hidden, residual, layer.post_norm)
-            hidden = self._linear(self._swiglu(self._linear(x, layer.gate_up)), layer.down)
+            hidden = self._linear(self._ffn_gate(x, layer.gate_up), layer.down)
         return self._norm(hidden, residual, self.final_norm)[0]
 
     def compute_logits(self, hidden, metadata):

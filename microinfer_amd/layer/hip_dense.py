@@ -69,6 +69,30 @@ def hip_linear(x: torch.Tensor, weight: torch.Tensor, *,
     return out
 
 
+def hip_linear_swiglu(x: torch.Tensor, gate_up: torch.Tensor, *,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """``F.silu(gate) * up`` of ``gate, up = F.linear(x, gate_up).chunk(2, -1)``
+    (``FFN.forward``, transformer.py:82-88) in one launch: ``gate_up [2 I, k]``
+    holds the gate's rows then the up projection's; the result ``[m, I]`` is
+    ``hip_silu_mul(hip_linear(x, gate_up))`` bit for bit."""
+    _lib.require_device(x, gate_up, out, what="gate/up projection")
+    if not supported_linear(x, gate_up) or gate_up.shape[0] % 32:
+        raise ValueError("hip_linear_swiglu: x [m <= 64, k] and gate_up [2 I, k] (I % 16 == 0, "
+                         "k % 32 == 0) of one 16-bit dtype with 16-byte aligned rows are "
+                         "required")
+    m, k = x.shape
+    inter = gate_up.shape[0] // 2
+    if out is None:
+        out = torch.empty((m, inter), dtype=x.dtype, device=x.device)
+    elif out.shape != (m, inter) or out.dtype != x.dtype or not _rows_aligned(out):
+        raise ValueError("hip_linear_swiglu: out must be [m, I] of x's dtype with aligned rows")
+    _lib.check(_lib.load().mi_linear_swiglu(
+        x.data_ptr(), x.stride(0), gate_up.data_ptr(), gate_up.stride(0), out.data_ptr(),
+        out.stride(0), m, inter, k, _lib.dtype_code(x.dtype), _lib.stream_handle(x.device)),
+        "mi_linear_swiglu")
+    return out
+
+
 def supported_rows(*tensors: torch.Tensor) -> bool:
     """Whether the norm / SwiGLU kernels take these ``[rows, dim]`` tensors."""
     first = tensors[0]

@@ -134,3 +134,9 @@ def test_dense_ops_validate_before_launch():
     assert lib.mi_silu_mul(fake, 6144, fake, 3072, 4, 3070, 2, None) == 1
     assert lib.mi_silu_mul(fake, 6000, fake, 3072, 4, 3072, 2, None) == 1
     assert lib.mi_silu_mul(None, 0, None, 0, 0, 3072, 2, None) == 0
+    # fused gate/up + SwiGLU: inter not a multiple of 16, output stride below
+    # inter, more than 64 rows, an empty batch
+    assert lib.mi_linear_swiglu(fake, 1024, fake, 1024, fake, 3072, 8, 3064, 1024, 2, None) == 1
+    assert lib.mi_linear_swiglu(fake, 1024, fake, 1024, fake, 3000, 8, 3072, 1024, 2, None) == 1
+    assert lib.mi_linear_swiglu(fake, 1024, fake, 1024, fake, 3072, 65, 3072, 1024, 2, None) == 2
+    assert lib.mi_linear_swiglu(None, 0, None, 0, None, 0, 0, 3072, 1024, 2, None) == 0

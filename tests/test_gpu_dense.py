@@ -14,7 +14,8 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from microinfer_amd.layer.hip_dense import hip_linear, hip_rms_norm_residual, hip_silu_mul
+from microinfer_amd.layer.hip_dense import (hip_linear, hip_linear_swiglu, hip_rms_norm_residual,
+                                            hip_silu_mul)
 from microinfer_amd.runner import capture_graph
 
 pytestmark = pytest.mark.gpu
@@ -57,6 +58,20 @@ def test_linear_matches_float32(m, n, k):
     y = hip_linear(x, w)
     _assert_close(y, _reference(x, w))
     assert torch.equal(hip_linear(x, w), y)  # reproducible
+
+
+@pytest.mark.parametrize("m,n,k", [(2, 32768, 64), (2, 32768, 96), (2, 4096, 64), (16, 4096, 416),
+                                   (20, 8192, 96), (40, 2048, 160), (64, 6144, 224)])
+def test_linear_partial_chunks(m, n, k):
+    """k ranges that leave a wave a partial chunk of k-steps (or none), under
+    every workgroup shape the launcher picks (4 or 8 waves, 16 or 32
+    columns, row-tiled or not)."""
+    torch.manual_seed(m + n + k)
+    x = torch.randn(m, k, device=DEV).to(torch.bfloat16)
+    w = (0.05 * torch.randn(n, k, device=DEV)).to(torch.bfloat16)
+    y = hip_linear(x, w)
+    assert not bool(torch.isnan(y).any())
+    _assert_close(y, _reference(x, w))
 
 
 def test_linear_f16_and_strided_rows():
@@ -145,3 +160,38 @@ def test_silu_mul_matches_torch(dtype, rows, inter):
     ref = F.silu(gate.float()) * up.float()
     err = (out.float() - ref).abs()
     assert bool((err <= 1.6e-2 * ref.abs() + 1e-6).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [1, 7, 16, 33, 64])
+@pytest.mark.parametrize("inter,k", [(3072, 1024), (12288, 4096), (16, 64), (2048, 96)])
+def test_linear_swiglu_is_projection_then_gate(dtype, m, inter, k):
+    """The fused launch equals hip_silu_mul(hip_linear(x, gate_up)) bit for
+    bit (same sums, same rounding steps), and F.silu(gate) * up of the
+    float32 product within the 16-bit roundings."""
+    torch.manual_seed(m * 31 + inter + k)
+    x = torch.randn(m, k, device=DEV).to(dtype)
+    w = (0.05 * torch.randn(2 * inter, k, device=DEV)).to(dtype)
+    fused = hip_linear_swiglu(x, w)
+    assert fused.shape == (m, inter)
+    assert torch.equal(fused, hip_silu_mul(hip_linear(x, w)))
+    gate, up = _reference(x, w).chunk(2, dim=-1)
+    ref = F.silu(gate) * up
+    err = (fused.float() - ref).abs()
+    assert bool((err <= 2.5e-2 * ref.abs() + 2e-3 * ref.abs().max() + 1e-6).all())
+    assert torch.equal(hip_linear_swiglu(x, w), fused)  # reproducible
+
+
+def test_linear_swiglu_rejects_and_strides():
+    w = torch.randn(6144, 1024, device=DEV).to(torch.bfloat16)
+    with pytest.raises(ValueError):
+        hip_linear_swiglu(torch.randn(65, 1024, device=DEV).to(torch.bfloat16), w)
+    with pytest.raises(ValueError):
+        hip_linear_swiglu(torch.randn(8, 1024, device=DEV).to(torch.bfloat16), w[:6128])
+    torch.manual_seed(9)
+    base = torch.randn(24, 1024 + 64, device=DEV).to(torch.bfloat16)
+    x = base[:, 64:]
+    out = torch.empty(24, 3072 + 32, device=DEV, dtype=torch.bfloat16)[:, :3072]
+    y = hip_linear_swiglu(x, w, out=out)
+    assert y.data_ptr() == out.data_ptr()
+    assert torch.equal(y, hip_silu_mul(hip_linear(x.contiguous(), w)))
