@@ -334,9 +334,9 @@ def test_hipgraph_replay_tracks_new_contexts():
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (8, 4, 64), (4, 1, 128)])
 def test_many_sequences_take_half_width_groups(dtype, hq, hkv, d):
-    # More (sequence, KV head) pairs than the device has CUs: the launch uses
-    # 4-wave workgroups. Adaptive and forced splits, and the fused append,
-    # must still match the oracle.
+    # More (sequence, KV head) pairs than the device has CUs: the launch runs
+    # two workgroups per CU (one ring slot per wave). Adaptive and forced
+    # splits, and the fused append, must still match the oracle.
     rng = np.random.default_rng(11)
     num_seqs, bs = 300 // hkv + 40, 16
     contexts = rng.integers(1, 400, num_seqs)
