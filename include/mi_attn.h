@@ -49,7 +49,9 @@ enum {
 /* Description of the last failure on the calling thread ("" after success). */
 const char* mi_last_error(void);
 
-/* ABI version of this library (major * 100 + minor). */
+/* ABI version of this library (major * 100 + minor). 101: mi_tune_decode and
+ * its plan/workspace knobs were removed (workspace and plan sizes depend only
+ * on the call's arguments). */
 int32_t mi_abi_version(void);
 
 /*

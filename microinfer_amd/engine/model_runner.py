@@ -8,7 +8,8 @@ eagerly when no bucket fits or graphs are off; greedy rows take the argmax,
 the others the temperature sampler, mixed per row as the reference does.
 
 The KV pool has one block more than the block manager hands out: the pad
-rows of graph buckets write their K/V there.
+rows of graph buckets write their K/V there. With ``EngineConfig.debug_mode``
+each step's metadata is validated before launch (``runner.validate_step``).
 """
 
 from __future__ import annotations
@@ -31,7 +32,10 @@ class ModelRunner:
                                 c.head_dim, dtype=model.dtype, device=model.device,
                                 layout=layout)
         model.bind_caches([self.kv_cache.layer(i) for i in range(c.num_hidden_layer)])
-        self.builder = StepMetadataBuilder(block_size, model.device, pad_block_id=num_blocks)
+        self.builder = StepMetadataBuilder(block_size, model.device, pad_block_id=num_blocks,
+                                           debug_mode=config.debug_mode, num_blocks=num_blocks,
+                                           max_pos_embed=c.max_pos_embed,
+                                           vocab_size=c.vocab_size)
         self.sampler = Sampler()
         self.graphs = None
         if config.use_cuda_graph:

@@ -10,9 +10,9 @@ here every route is a gfx950 kernel and nothing falls back to the CPU:
   so the reference's ``Σctx >= 4 Σq`` choice between in-place and gathered
   prefill, :104-139, disappears)
 
-``gather_paged_kv`` keeps the reference's signature for callers that need
-contiguous varlen K/V; it is one launch instead of two ``index_select`` per
-request plus ``cat``.
+``gather_paged_kv`` (also under the reference's name ``_gather_paged_kv``)
+keeps the reference's signature for callers that need contiguous varlen K/V;
+it is one launch instead of two ``index_select`` per request plus ``cat``.
 """
 
 from __future__ import annotations
@@ -48,6 +48,10 @@ def gather_paged_kv(key_cache, value_cache, block_tables, contexts, block_size):
         offsets.append(offsets[-1] + length)
     cu_k = torch.tensor(offsets, dtype=torch.int32, device=key_cache.device)
     return hip_gather_kv(key_cache, value_cache, block_tables[: len(contexts)], cu_k, offsets[-1])
+
+
+# The reference's name (paged_attention.py:76), for callers bound to it.
+_gather_paged_kv = gather_paged_kv
 
 
 def paged_attention_meta(

@@ -71,6 +71,125 @@ def graph_buckets(max_num_seqs: int) -> list[int]:
     return buckets
 
 
+def _host_ints(tensor) -> list[int]:
+    return [int(v) for v in tensor.reshape(-1).tolist()]
+
+
+def validate_step(seqs, input_ids, positions, metadata, is_prefill: bool, *, block_size: int,
+                  num_blocks: int | None = None, max_pos_embed: int | None = None,
+                  vocab_size: int | None = None) -> None:
+    """Debug-mode check of one step's metadata against the scheduled sequences.
+
+    Restates ``ModelRunner.validate_step`` (microinfer/runner.py:387-528):
+    the same invariants, raised as ValueError with the reference's messages,
+    before anything is launched. The device-built tensors are read back once
+    (a synchronising copy), which is why this runs only in debug mode.
+    ``num_blocks`` is the pool the scheduler hands out, ``max_pos_embed`` and
+    ``vocab_size`` the model's limits (each check is skipped when None).
+    """
+    if metadata.is_prefill is not is_prefill:
+        raise ValueError("metadata mode does not match scheduled work")
+    if input_ids.ndim != 1 or positions.ndim != 1:
+        raise ValueError("input_ids and positions must be 1-D")
+    if input_ids.numel() != positions.numel() or input_ids.numel() == 0:
+        raise ValueError("input_ids/positions must be nonempty and equal length")
+    if not seqs:
+        raise ValueError("a scheduled batch must contain requests")
+    slots = metadata.slot_mapping
+    if slots is None or slots.ndim != 1 or slots.numel() != input_ids.numel():
+        raise ValueError("slot_mapping must match scheduled tokens")
+    slot_list, pos_list, id_list = _host_ints(slots), _host_ints(positions), _host_ints(input_ids)
+    if min(slot_list) < 0:
+        raise ValueError("slot_mapping must be nonnegative")
+    if len(set(slot_list)) != len(slot_list):
+        raise ValueError("slot_mapping contains duplicate slots")
+    if num_blocks is not None and max(slot_list) >= num_blocks * block_size:
+        raise ValueError("slot_mapping exceeds KV capacity")
+    if min(pos_list) < 0:
+        raise ValueError("positions must be nonnegative")
+    if max_pos_embed is not None and max(pos_list) >= max_pos_embed:
+        raise ValueError("position exceeds model max_pos_embed")
+    if min(id_list) < 0:
+        raise ValueError("input_ids must be nonnegative")
+    if vocab_size is not None and max(id_list) >= vocab_size:
+        raise ValueError("input_ids exceed model vocabulary")
+
+    def covered(ids, needed: int, short_message: str) -> None:
+        if len(ids) < needed:
+            raise ValueError(short_message)
+        for block_id in ids[:needed]:
+            if int(block_id) < 0:
+                raise ValueError("block table contains a negative block id")
+            if num_blocks is not None and int(block_id) >= num_blocks:
+                raise ValueError("block id exceeds KV pool")
+
+    def slot_of(seq, position: int) -> int:
+        return int(seq.block_table[position // block_size]) * block_size + position % block_size
+
+    # Per request: the context the step's attention reads (cached + scheduled
+    # tokens for prefill, the whole sequence for decode).
+    contexts = []
+    if is_prefill:
+        if metadata.cu_seqlens_q is None or metadata.cu_seqlens_k is None:
+            raise ValueError("prefill requires cu_seqlens_q/cu_seqlens_k")
+        cu_q, cu_k = _host_ints(metadata.cu_seqlens_q), _host_ints(metadata.cu_seqlens_k)
+        if len(cu_q) != len(seqs) + 1 or len(cu_k) != len(seqs) + 1:
+            raise ValueError("cu_seqlens must contain num_requests + 1 entries")
+        if cu_q[0] != 0 or cu_k[0] != 0 or cu_q[-1] != input_ids.numel():
+            raise ValueError("invalid cu_seqlens endpoints")
+        q_lens = [b - a for a, b in zip(cu_q, cu_q[1:])]
+        k_lens = [b - a for a, b in zip(cu_k, cu_k[1:])]
+        for i, seq in enumerate(seqs):
+            start = seq.num_cached_tokens
+            end = start + seq.num_scheduled_tokens
+            if q_lens[i] <= 0:
+                raise ValueError("prefill query length must be positive")
+            if q_lens[i] != seq.num_scheduled_tokens:
+                raise ValueError("query length does not match scheduled tokens")
+            if k_lens[i] != end:
+                raise ValueError("KV length does not match cached+scheduled tokens")
+            if len(seq) < end:
+                raise ValueError("scheduled tokens exceed sequence length")
+            covered(seq.block_table, -(-end // block_size),
+                    "block table does not cover scheduled tokens")
+            if pos_list[cu_q[i]:cu_q[i + 1]] != list(range(start, end)):
+                raise ValueError("positions do not match prefill range")
+            if slot_list[cu_q[i]:cu_q[i + 1]] != [slot_of(seq, p) for p in range(start, end)]:
+                raise ValueError("slot_mapping does not match block table")
+            contexts.append(end)
+        if cu_q[-1] != sum(q_lens) or cu_k[-1] != sum(k_lens):
+            raise ValueError("cu_seqlens totals do not match")
+        if metadata.max_seqlen_q != max(q_lens):
+            raise ValueError("max_seqlen_q does not match cu_seqlens_q")
+        if metadata.max_seqlen_k != max(k_lens):
+            raise ValueError("max_seqlen_k does not match cu_seqlens_k")
+        if any(seq.num_cached_tokens for seq in seqs) and metadata.block_tables is None:
+            raise ValueError("cached prefixes require block_tables")
+    else:
+        if len(seqs) != input_ids.numel():
+            raise ValueError("decode needs exactly one token per request")
+        if metadata.context_lens is None or metadata.context_lens.numel() != len(seqs):
+            raise ValueError("decode requires one context length per request")
+        if metadata.block_tables is None:
+            raise ValueError("decode requires block_tables")
+        for i, (seq, context) in enumerate(zip(seqs, _host_ints(metadata.context_lens))):
+            if context != len(seq) or context <= 0:
+                raise ValueError("context length does not match sequence length")
+            if pos_list[i] != context - 1:
+                raise ValueError("decode position does not match context length")
+            covered(seq.block_table, -(-context // block_size),
+                    "block table does not cover scheduled tokens")
+            if slot_list[i] != slot_of(seq, context - 1):
+                raise ValueError("decode slot does not match block table")
+            contexts.append(context)
+    tables = metadata.block_tables
+    if tables is not None:
+        if tables.ndim != 2 or tables.shape[0] != len(seqs):
+            raise ValueError("block_tables must be [num_requests, max_blocks]")
+        for row, context in zip(tables.tolist(), contexts):
+            covered(row, -(-context // block_size), "block table does not cover context")
+
+
 class DecodeBuffers:
     """Device tensors a decode step writes its metadata into.
 
@@ -161,14 +280,25 @@ class StepMetadataBuilder:
     ``pad_block_id`` is the block a graph runner reserves past the scheduler's
     pool for pad rows (``allocate_kv_cache``, microinfer/runner.py:134-153);
     it is only needed for graph buckets.
+
+    With ``debug_mode`` every step is checked by ``validate_step`` before it
+    is returned (and so before anything reads it), against ``num_blocks``,
+    ``max_pos_embed`` and ``vocab_size`` where given, and the metadata asks
+    for checked cache writes, as the reference's debug mode does
+    (microinfer/runner.py:337-346, :378-384).
     """
 
-    def __init__(self, block_size: int, device, *, pad_block_id: int | None = None):
+    def __init__(self, block_size: int, device, *, pad_block_id: int | None = None,
+                 debug_mode: bool = False, num_blocks: int | None = None,
+                 max_pos_embed: int | None = None, vocab_size: int | None = None):
         if block_size <= 0:
             raise ValueError("block_size must be positive")
         self.block_size = block_size
         self.device = torch.device(device)
         self.pad_block_id = pad_block_id
+        self.debug_mode = debug_mode
+        self.limits = dict(block_size=block_size, num_blocks=num_blocks,
+                           max_pos_embed=max_pos_embed, vocab_size=vocab_size)
         self._upload = _Upload(self.device)
         self._decode_buffers: DecodeBuffers | None = None
         self._decode_upload: torch.Tensor | None = None
@@ -260,8 +390,10 @@ class StepMetadataBuilder:
             max_seqlen_k=int(ends.max()) if n else 0,
             slot_mapping=slots,
             block_tables=block_tables,
-            validate_cache_write=False,
+            validate_cache_write=self.debug_mode,
         )
+        if self.debug_mode:
+            self.validate(seqs, input_ids, positions, metadata, True)
         return input_ids, positions, metadata
 
     # -- decode ---------------------------------------------------------------
@@ -334,9 +466,15 @@ class StepMetadataBuilder:
             slot_mapping=buffers.slot_mapping[:n],
             context_lens=buffers.context_lens[:n],
             block_tables=buffers.block_tables[:n],
-            validate_cache_write=False,
+            validate_cache_write=self.debug_mode,
         )
+        if self.debug_mode:
+            self.validate(seqs, buffers.input_ids[:n], buffers.positions[:n], metadata, False)
         return buffers.input_ids[:n], buffers.positions[:n], metadata
+
+    def validate(self, seqs, input_ids, positions, metadata, is_prefill: bool) -> None:
+        """``validate_step`` with this builder's block size and limits."""
+        validate_step(seqs, input_ids, positions, metadata, is_prefill, **self.limits)
 
     def pad_buffers(self, batch: int, width: int) -> DecodeBuffers:
         """Fresh bucket buffers holding only pad rows (``_fill_pad_buffers``,
@@ -422,8 +560,13 @@ class DecodeGraphRunner:
             return None
         batch, buffers, graph, out = bucket
         self.builder.fill_decode(buffers, seqs, rows=batch)
-        graph.replay()
         n = len(seqs)
+        if self.builder.debug_mode:
+            # The batch's rows as the graph will read them (microinfer/
+            # runner.py:582-598).
+            self.builder.validate(seqs, buffers.input_ids[:n], buffers.positions[:n],
+                                  buffers.metadata(n), False)
+        graph.replay()
         if self.greedy:
             return out[0][:n], out[1][:n]
         return out[:n]

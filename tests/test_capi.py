@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_clean_error_state():
     lib = _lib.load()
-    assert lib.mi_abi_version() == 100
+    assert lib.mi_abi_version() == 101
     assert isinstance(_lib.last_error(), str)
 
 
@@ -140,3 +140,18 @@ def test_dense_ops_validate_before_launch():
     assert lib.mi_linear_swiglu(fake, 1024, fake, 1024, fake, 3000, 8, 3072, 1024, 2, None) == 1
     assert lib.mi_linear_swiglu(fake, 1024, fake, 1024, fake, 3072, 65, 3072, 1024, 2, None) == 2
     assert lib.mi_linear_swiglu(None, 0, None, 0, None, 0, 0, 3072, 1024, 2, None) == 0
+
+
+def test_noalloc_refuses_calls_beyond_its_scratch():
+    # The size check returns before any HIP call (no device lookup, no
+    # launch), so the placeholder pointers are never dereferenced.
+    lib = _lib.load()
+    room = lib.mi_paged_decode_noalloc_max_bytes()
+    assert room > 0
+    # 4096 sequences of a 128-query-head layer need far more than the scratch.
+    assert lib.mi_paged_decode_workspace_bytes(4096, 128, 16, 256, 0) > room
+    fake = 256
+    status = lib.mi_paged_decode_append_noalloc(
+        fake, 4096, 256, fake, 4096, 256, fake, 32768, 256, fake, fake, 65536, 4096, 256,
+        fake, 1, 1, fake, fake, 32768, 256, 4096, 128, 16, 256, 16, 64, 0, 1.0, 2, None)
+    assert status == 3 and "scratch" in _lib.last_error()

@@ -202,3 +202,71 @@ def test_text_from_a_tokenizer(scheduler_factory):
         await frontend.stop()
 
     asyncio.run(scenario())
+
+
+class StepInterrupted(BaseException):
+    """Not an Exception: what a cancellation or interrupt raising in a step looks like."""
+
+
+def test_base_exception_in_a_step_ends_every_stream(scheduler_factory):
+    # The engine thread catches BaseException too: every admitted request's
+    # consumer gets a terminal "abort" event (none waits forever), the engine
+    # is left empty, and the thread serves the next request.
+    engine, runner, manager = make_engine(scheduler_factory, num_blocks=16)
+    run = runner.run
+
+    def interrupted(seqs, is_prefill):
+        if runner.calls >= 1:
+            runner.calls += 1
+            raise StepInterrupted("interrupted mid-step")
+        return run(seqs, is_prefill)
+
+    runner.run = interrupted
+
+    async def scenario():
+        frontend = AsyncEngine(engine, max_waiting=8)
+        a = await frontend.add_request([1, 2], params(5))
+        b = await frontend.add_request([3], params(5))
+        outs = await asyncio.wait_for(asyncio.gather(frontend.collect(a), frontend.collect(b)), 10)
+        assert all(o.finished and o.finish_reason == "abort" for o in outs)
+        assert "interrupted" in frontend.stats()["last_error"]
+        assert engine.is_finished() and not manager.used_block_ids
+        runner.run = run
+        again = await asyncio.wait_for(frontend.generate([4], params(2)), 10)
+        assert again.finish_reason == "length" and len(again.token_ids) == 2
+        await frontend.stop()
+
+    asyncio.run(scenario())
+
+
+def test_stop_during_a_step_ends_every_stream(scheduler_factory):
+    # stop() while the engine thread is inside a step: the step finishes, the
+    # thread then aborts what is left, and every consumer gets "abort".
+    engine, runner, manager = make_engine(scheduler_factory, num_blocks=16)
+    armed, entered, release = threading.Event(), threading.Event(), threading.Event()
+    run = runner.run
+
+    def slow(seqs, is_prefill):
+        if armed.is_set():  # the first step after every admission
+            entered.set()
+            release.wait(10)
+        return run(seqs, is_prefill)
+
+    runner.run = slow
+
+    async def scenario():
+        frontend = AsyncEngine(engine, max_waiting=8)
+        requests = [await frontend.add_request([i + 1], params(50)) for i in range(3)]
+        armed.set()
+        consumers = [asyncio.ensure_future(frontend.collect(r)) for r in requests]
+        await asyncio.get_running_loop().run_in_executor(None, entered.wait, 10)
+        stopping = asyncio.ensure_future(frontend.stop())
+        await asyncio.sleep(0.05)
+        release.set()
+        await asyncio.wait_for(stopping, 10)
+        outs = await asyncio.wait_for(asyncio.gather(*consumers), 10)
+        assert all(o.finished and o.finish_reason == "abort" for o in outs)
+        assert engine.is_finished() and not manager.used_block_ids
+        assert frontend.stats()["active_requests"] == 0
+
+    asyncio.run(scenario())

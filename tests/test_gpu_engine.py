@@ -63,20 +63,24 @@ def prompts(seed, lengths, vocab=512):
 
 
 def check_against_oracle(model, prompt_list, outputs, max_tokens, tolerance):
-    """Teacher-forced check of every emitted token; returns how many were
-    checked. At each position the oracle's logit of the engine's token must
-    be within ``tolerance`` of the oracle's best logit there: equal to its
-    greedy choice, or a near-tie that other rounding may flip."""
+    """Teacher-forced check of every emitted token; returns ``(checked,
+    exact)``: how many positions were checked and at how many the engine's
+    token IS the oracle's greedy choice. At each position the oracle's logit
+    of the engine's token must be within ``tolerance`` of the oracle's best
+    logit there: equal to its greedy choice, or a near-tie that other
+    rounding may flip."""
     weights = weights_f64(model.host_weights())
-    checked = 0
+    checked = exact = 0
     for prompt, got in zip(prompt_list, outputs):
         assert len(got) == max_tokens, f"prompt len {len(prompt)}: {len(got)} tokens"
         deficits = token_deficits(weights, model.config, prompt, got)
         for i, (tok, deficit) in enumerate(zip(got, deficits)):
             checked += 1
+            exact += deficit == 0.0
             assert deficit <= tolerance, (f"prompt len {len(prompt)}: token {i} ({tok}) is "
                                           f"{deficit:.4g} below the oracle's best logit")
-    return checked
+    print(f"teacher-forced: {exact} of {checked} tokens are the oracle's exact argmax")
+    return checked, exact
 
 
 @pytest.fixture(scope="module")
@@ -90,7 +94,7 @@ def test_greedy_tokens_match_dense_oracle(tiny_model, graph, mixed):
     engine = make_engine(tiny_model, use_cuda_graph=graph, mixed_batch=mixed)
     batch = prompts(1, [1, 7, 16, 17, 33, 40])
     out = engine.generate(batch, GREEDY)
-    assert check_against_oracle(tiny_model, batch, out, 6, 1e-4) == 36
+    assert check_against_oracle(tiny_model, batch, out, 6, 1e-4) == (36, 36)
     stats = engine.stats()
     assert stats["num_steps"] > 6 and stats["used_blocks"] == 0
     if mixed:
@@ -104,7 +108,7 @@ def test_prefix_cache_reuse_keeps_tokens(tiny_model):
     follow = [base[:32] + prompts(3, [5])[0], list(base)]
     out = engine.generate(follow, GREEDY)
     assert engine.stats()["prefix_cache_hit_blocks"] >= 4
-    assert check_against_oracle(tiny_model, follow, out, 6, 1e-4) == 12
+    assert check_against_oracle(tiny_model, follow, out, 6, 1e-4) == (12, 12)
 
 
 def test_preemption_keeps_tokens(tiny_model):
@@ -114,7 +118,7 @@ def test_preemption_keeps_tokens(tiny_model):
     params = SampleParameter(max_tokens=12, greedy=True)
     out = engine.generate(batch, params)
     assert engine.stats()["num_preemptions"] > 0
-    assert check_against_oracle(tiny_model, batch, out, 12, 1e-4) == 36
+    assert check_against_oracle(tiny_model, batch, out, 12, 1e-4) == (36, 36)
 
 
 def test_sampled_and_greedy_rows_in_one_batch(tiny_model):
@@ -124,7 +128,7 @@ def test_sampled_and_greedy_rows_in_one_batch(tiny_model):
     out = engine.generate(batch, params)
     assert all(len(o) == 6 and all(0 <= t < TINY.vocab_size for t in o) for o in out)
     greedy = [batch[0], batch[2]]
-    assert check_against_oracle(tiny_model, greedy, [out[0], out[2]], 6, 1e-4) == 12
+    assert check_against_oracle(tiny_model, greedy, [out[0], out[2]], 6, 1e-4) == (12, 12)
 
 
 def test_bf16_qwen3_layers_match_oracle():
@@ -137,7 +141,8 @@ def test_bf16_qwen3_layers_match_oracle():
     # bf16 weights are exact in the oracle; activations round at every
     # product (logit spread about 1.6), so a token may sit up to 0.1 below
     # the oracle's best logit.
-    assert check_against_oracle(model, batch, out, 6, 0.1) == 36
+    checked, exact = check_against_oracle(model, batch, out, 6, 0.1)
+    assert checked == 36 and exact >= 34
 
 
 def test_engine_rejects_requests_beyond_capacity(tiny_model):
@@ -155,7 +160,8 @@ def test_qwen3_06b_engine_matches_oracle():
                          max_num_prefill_tokens=512)
     batch = prompts(5, [128, 64, 17, 100], vocab=151936)
     out = engine.generate(batch, SampleParameter(max_tokens=4, greedy=True))
-    assert check_against_oracle(model, batch, out, 4, QWEN3_06B_TOLERANCE) == 16
+    checked, exact = check_against_oracle(model, batch, out, 4, QWEN3_06B_TOLERANCE)
+    assert checked == 16 and exact >= 15
 
 
 def test_engine_workload_matches_oracle_teacher_forced():
@@ -178,9 +184,13 @@ def test_engine_workload_matches_oracle_teacher_forced():
     assert stats["num_mixed_steps"] + stats["num_decode_steps"] >= ENGINE_OUTPUT_LEN - 1
     assert stats["used_blocks"] == 0
     picked = list(range(0, len(batch), 4))
-    checked = check_against_oracle(model, [batch[i] for i in picked], [out[i] for i in picked],
-                                   ENGINE_OUTPUT_LEN, QWEN3_06B_TOLERANCE)
+    checked, exact = check_against_oracle(model, [batch[i] for i in picked],
+                                          [out[i] for i in picked], ENGINE_OUTPUT_LEN,
+                                          QWEN3_06B_TOLERANCE)
     assert checked == 16 * ENGINE_OUTPUT_LEN
+    # Near-ties aside, the tokens ARE the oracle's greedy tokens: at least
+    # 95 % of the 256 positions are its exact argmax.
+    assert exact >= 0.95 * checked, f"only {exact} of {checked} exact"
 
 
 def test_async_engine_on_a_side_stream_matches_generate(tiny_model):
@@ -215,4 +225,28 @@ def test_async_engine_on_a_side_stream_matches_generate(tiny_model):
     torch.cuda.synchronize()
     assert [list(o.token_ids) for o in outs] == expected
     assert seen and all(seen)
-    assert check_against_oracle(tiny_model, batch, expected, 6, 1e-4) == 12
+    assert check_against_oracle(tiny_model, batch, expected, 6, 1e-4) == (12, 12)
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_debug_mode_validates_every_step_and_keeps_tokens(tiny_model, graph, monkeypatch):
+    # EngineConfig.debug_mode: every prefill, eager decode and graph-bucket
+    # decode step goes through runner.validate_step (microinfer/runner.py:
+    # 387-528) before launch, and the tokens do not change.
+    import microinfer_amd.runner as runner_module
+
+    seen = []
+    real = runner_module.validate_step
+
+    def recording(seqs, input_ids, positions, metadata, is_prefill, **limits):
+        seen.append(is_prefill)
+        assert limits["num_blocks"] == 64 and limits["vocab_size"] == TINY.vocab_size
+        return real(seqs, input_ids, positions, metadata, is_prefill, **limits)
+
+    monkeypatch.setattr(runner_module, "validate_step", recording)
+    batch = prompts(1, [1, 7, 16, 17, 33, 40])
+    expected = make_engine(tiny_model, use_cuda_graph=graph).generate(batch, GREEDY)
+    assert not seen
+    engine = make_engine(tiny_model, use_cuda_graph=graph, debug_mode=True)
+    assert engine.generate(batch, GREEDY) == expected
+    assert True in seen and False in seen

@@ -5,7 +5,8 @@ Both run the same kernels and, given the same context lengths, the same
 partition plan, so outputs and appended cache rows must be bit-identical.
 Two calls in a row share the library's static scratch: the second is
 smaller (fewer sequences, shorter contexts) and must not see the first
-call's leftovers. Oversized calls are refused before any launch.
+call's leftovers. A captured call replays with new context lengths.
+(Oversized calls are refused before any HIP call: tests/test_capi.py.)
 """
 
 import math
@@ -71,14 +72,48 @@ def test_noalloc_matches_the_workspace_entry_point_twice():
     one_case(5, 16, 700, seed=1)     # smaller: fewer sequences, shorter contexts
 
 
-def test_noalloc_refuses_calls_beyond_its_scratch():
-    lib = _lib.load()
-    room = lib.mi_paged_decode_noalloc_max_bytes()
-    assert room > 0
-    # 4096 sequences of a 128-query-head layer need far more than the scratch.
-    assert lib.mi_paged_decode_workspace_bytes(4096, 128, 16, 256, 0) > room
-    fake = 256
-    status = lib.mi_paged_decode_append_noalloc(
-        fake, 4096, 256, fake, 4096, 256, fake, 32768, 256, fake, fake, 65536, 4096, 256,
-        fake, 1, 1, fake, fake, 32768, 256, 4096, 128, 16, 256, 16, 64, 0, 1.0, 2, None)
-    assert status == 3 and "scratch" in _lib.last_error()
+def test_noalloc_under_graph_capture_tracks_context_lens():
+    # Captured once (after an eager call has looked up this device's scratch),
+    # replayed with two different context_lens: the plan kernel inside the
+    # graph re-plans from the new lengths and re-zeroes its counters, so each
+    # replay equals the workspace entry point run eagerly on the same inputs,
+    # bit for bit (output and appended cache rows).
+    from microinfer_amd.runner import capture_graph
+
+    pool, num_seqs, width = 2048, 12, 64
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    cache = KVCache(1, pool, 16, 8, 128, dtype=torch.bfloat16, device=DEV)
+    cache.keys[0].copy_(torch.randn(cache.keys[0].shape, generator=gen, device=DEV))
+    cache.values[0].copy_(torch.randn(cache.values[0].shape, generator=gen, device=DEV))
+    kc, vc = cache.keys[0], cache.values[0]
+    ref_k, ref_v = kc.clone(), vc.clone()
+    q = torch.randn((num_seqs, 16, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    new_k = torch.randn((num_seqs, 8, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    new_v = torch.randn((num_seqs, 8, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    tables = torch.randperm(pool, generator=torch.Generator().manual_seed(5))[
+        :num_seqs * width].to(torch.int32).reshape(num_seqs, width).to(DEV)
+    lens = torch.full((num_seqs,), 100, dtype=torch.int32, device=DEV)
+    scale = 1 / math.sqrt(128)
+    noalloc_decode(new_k, new_v, q, kc, vc, tables, lens, scale)  # eager: scratch looked up
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with capture_graph(graph, stream=side):
+        out = noalloc_decode(new_k, new_v, q, kc, vc, tables, lens, scale)
+    torch.cuda.synchronize()
+    rng = torch.Generator().manual_seed(6)
+    for lo, hi in ((900, 1024), (1, 300)):
+        print(f"replay: contexts U[{lo},{hi}]", flush=True)
+        lens.copy_(torch.randint(lo, hi + 1, (num_seqs,), generator=rng, dtype=torch.int32))
+        ref_k.copy_(kc)
+        ref_v.copy_(vc)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        expected = hip_paged_decode(q, ref_k, ref_v, tables, lens, scale=scale, new_keys=new_k,
+                                    new_values=new_v)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), expected.view(torch.int16))
+        assert torch.equal(kc.view(torch.int16), ref_k.view(torch.int16))
+        assert torch.equal(vc.view(torch.int16), ref_v.view(torch.int16))
