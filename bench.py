@@ -268,10 +268,8 @@ def measured_bf16_gemm_peak(torch, n: int = 8192, runs: int = 20) -> dict:
             "us": round(ms * 1e3, 1)}
 
 
-def run_prefill(args) -> int:
-    """Mixed chunked prefill (8B shape): one varlen launch per step."""
-    import torch
-
+def prefill_state(torch, layout: str) -> dict:
+    """The mixed chunked-prefill batch on the device (8B shape, pool 65536)."""
     from microinfer_amd.layer.hip_paged_attention import hip_paged_prefill
     from microinfer_amd.workloads import make_mixed_prefill_batch, prefill_flops
     from microinfer_amd.worker.kv_cache import KVCache
@@ -280,7 +278,7 @@ def run_prefill(args) -> int:
     dev = torch.device("cuda", 0)
     log("allocating the 8B-shape cache (65536 blocks)")
     cache = KVCache(1, batch.pool_blocks, 16, 8, 128, dtype=torch.bfloat16, device=dev,
-                    layout=args.layout)
+                    layout=layout)
     gen = torch.Generator(device=dev).manual_seed(0)
     cache.keys[0].copy_(torch.randn(cache.keys[0].shape, generator=gen, device=dev))
     cache.values[0].copy_(torch.randn(cache.values[0].shape, generator=gen, device=dev))
@@ -298,6 +296,36 @@ def run_prefill(args) -> int:
         return hip_paged_prefill(q, cache.keys[0], cache.values[0], cu_q, cu_k, tables,
                                  max_seqlen_q=max_q, scale=scale)
 
+    flops = prefill_flops(batch.q_lens, batch.context_lens, num_q_heads=32, head_dim=128)
+    return dict(batch=batch, cache=cache, q=q, gen=gen, step=step, flops=flops,
+                total_q=total_q, dev=dev)
+
+
+def time_launches(torch, run, args, steps: int) -> float:
+    """Milliseconds per ``run()`` after the warm-up, HIP events on the
+    current stream (the stream every launch goes to)."""
+    warm_up(torch, run, args)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        run()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def run_prefill(args) -> int:
+    """Mixed chunked prefill (8B shape): one varlen launch per step."""
+    import torch
+
+    from microinfer_amd.layer.hip_paged_attention import hip_paged_prefill
+    from microinfer_amd.workloads import prefill_flops
+
+    st = prefill_state(torch, args.layout)
+    batch, cache, q, gen, step, dev = (st[k] for k in ("batch", "cache", "q", "gen", "step",
+                                                        "dev"))
+    total_q = st["total_q"]
+    scale = 1 / math.sqrt(128)
     step()
     torch.cuda.synchronize()
     # A step is one launch: launched eagerly, back to back, the launches queue
@@ -310,17 +338,11 @@ def run_prefill(args) -> int:
         run = graph.replay
     else:
         run = step
-    warm_up(torch, run, args)
+    ms = time_launches(torch, run, args, args.steps)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(args.steps):
-        run()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
     if args.copy_calibration_mib:
         copy_calibration(torch, args.copy_calibration_mib)
-    flops = prefill_flops(batch.q_lens, batch.context_lens, num_q_heads=32, head_dim=128)
+    flops = st["flops"]
     tflops = flops / (ms * 1e-3) / 1e12
     log(f"{ms * 1e3:.1f} us per launch, {tflops:.1f} TFLOP/s")
     # Beside it, the no-prefix (direct) prefill on contiguous K/V: 8 prompts
@@ -1222,16 +1244,15 @@ def run_gather(args) -> int:
                       "launch"), "rows": total}, cpu, measured_traffic(GATHER_TRAFFIC))
 
 
-def run_long_decode(args) -> int:
-    """Long-context decode (Qwen3-8B heads: 32 Q / 8 KV, head_dim 128, bf16,
-    pool 65536 blocks of 16): 1 or 4 sequences of 4096 / 16384 / 32768
-    tokens, split into partitions merged in the same launch. Each case
-    replays launches over distinct blocks (more bytes than the last-level
-    cache holds) from a hipGraph; ``value`` is the 4 x 32768 case."""
-    import torch
+LONG_DECODE_CASES = ((1, 4096), (1, 16384), (1, 32768), (4, 4096), (4, 16384), (4, 32768))
 
+
+def time_long_decode(torch, args, which):
+    """Per-launch time of long-context decode cases ``(rows, ctx)`` (8B heads,
+    pool 65536 in the ``--layout`` cache): each case replays launches over
+    distinct blocks from a hipGraph. Returns (cache, kc, vc, perm, gen,
+    {"RxC": (us, algorithmic bytes)})."""
     from microinfer_amd.layer.hip_paged_attention import decode_plan, hip_paged_decode
-
     from microinfer_amd.worker.kv_cache import KVCache
 
     dev = torch.device("cuda", 0)
@@ -1246,25 +1267,37 @@ def run_long_decode(args) -> int:
     rng = np.random.default_rng(0)
     perm = torch.tensor(rng.permutation(num_blocks).astype(np.int32), device=dev)
     cases = {}
-    for rows in (1, 4):
-        for ctx in (4096, 16384, 32768):
-            nb = ctx // bs
-            launches = min(28, num_blocks // (rows * nb))
-            q = torch.randn((launches, rows, hq, d), generator=gen, device=dev).to(torch.bfloat16)
-            tables = [perm[i * rows * nb:(i + 1) * rows * nb].reshape(rows, nb).contiguous()
-                      for i in range(launches)]
-            lens = torch.full((rows,), ctx, dtype=torch.int32, device=dev)
+    for rows, ctx in which:
+        nb = ctx // bs
+        launches = min(28, num_blocks // (rows * nb))
+        q = torch.randn((launches, rows, hq, d), generator=gen, device=dev).to(torch.bfloat16)
+        tables = [perm[i * rows * nb:(i + 1) * rows * nb].reshape(rows, nb).contiguous()
+                  for i in range(launches)]
+        lens = torch.full((rows,), ctx, dtype=torch.int32, device=dev)
 
-            def many(q=q, tables=tables, lens=lens, launches=launches, nb=nb):
-                # One partition plan per step, shared by every layer's launch.
-                plan = decode_plan(lens, num_kv_heads=hkv, block_size=bs, block_table_width=nb)
-                for i in range(launches):
-                    hip_paged_decode(q[i], kc, vc, tables[i], lens, plan=plan)
+        def many(q=q, tables=tables, lens=lens, launches=launches, nb=nb):
+            # One partition plan per step, shared by every layer's launch.
+            plan = decode_plan(lens, num_kv_heads=hkv, block_size=bs, block_table_width=nb)
+            for i in range(launches):
+                hip_paged_decode(q[i], kc, vc, tables[i], lens, plan=plan)
 
-            us = _graph_time(torch, many, launches, max(1, args.steps // 5), args.warmup)
-            nbytes = rows * ctx * hkv * d * 2 * 2 + 2 * rows * hq * d * 2 + rows * nb * 4 + 8 * rows
-            cases[f"{rows}x{ctx}"] = (us, nbytes)
-            log(f"{rows} x {ctx}: {us:.2f} us per launch, {nbytes / us / 1e3:.0f} GB/s")
+        us = _graph_time(torch, many, launches, max(1, args.steps // 5), args.warmup)
+        nbytes = rows * ctx * hkv * d * 2 * 2 + 2 * rows * hq * d * 2 + rows * nb * 4 + 8 * rows
+        cases[f"{rows}x{ctx}"] = (us, nbytes)
+        log(f"{rows} x {ctx}: {us:.2f} us per launch, {nbytes / us / 1e3:.0f} GB/s")
+    return cache, kc, vc, perm, gen, cases
+
+
+def run_long_decode(args) -> int:
+    """Long-context decode (Qwen3-8B heads: 32 Q / 8 KV, head_dim 128, bf16,
+    pool 65536 blocks of 16): 1 or 4 sequences of 4096 / 16384 / 32768
+    tokens, split into partitions merged in the same launch. Each case
+    replays launches over distinct blocks (more bytes than the last-level
+    cache holds) from a hipGraph; ``value`` is the 4 x 32768 case."""
+    import torch
+
+    cache, kc, vc, perm, gen, cases = time_long_decode(torch, args, LONG_DECODE_CASES)
+    hq, hkv, d, bs, dev = 32, 8, 128, 16, kc.device
     us, nbytes = cases["4x32768"]
     achieved = nbytes / (us * 1e-6) / 1e9
     cpu = None
@@ -1374,11 +1407,109 @@ def main() -> int:
         cpu = engine_cpu_baseline(e["model"])
         cfg["cpu_decode_tok_s"] = cpu["value"]
         result["cpu_baseline_engine"] = cpu
+    del e
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    result.update(other_workloads(torch, args))
     print(json.dumps(result), flush=True)
     return 0
 
 
 ENGINE_BATCHES = 3
+DEFAULT_LONG_CASES = ((4, 32768), (1, 32768), (1, 16384))
+
+
+def other_workloads(torch, args) -> dict:
+    """The other workloads' figures, as extra keys of the default line: the
+    mixed chunked prefill (MFMA roofline), long-context split decode and the
+    small fp32 decode with its CPU oracle beside it."""
+    from microinfer_amd.workloads import QWEN3_06B, decode_bytes, make_decode_batch
+
+    out = {}
+    st = prefill_state(torch, args.layout)
+    st["step"]()
+    torch.cuda.synchronize()
+    ms = time_launches(torch, st["step"], args, 20)
+    tflops = st["flops"] / (ms * 1e-3) / 1e12
+    log(f"mixed prefill: {ms * 1e3:.1f} us per launch, {tflops:.1f} TFLOP/s")
+    out["prefill"] = {
+        "workload": ("mixed chunked prefill, Qwen3-8B attention (32 Q / 8 KV heads), bf16, "
+                     "block 16, pool 65536: 8 chunks of 512 rows on prefixes U[0,3072] "
+                     "(first 1024 tokens shared) + 24 decode rows, contexts U[256,2048], "
+                     "seed 0; one varlen launch, eager back to back, 20 timed"),
+        "tflops": round(tflops, 2), "us_per_launch": round(ms * 1e3, 3),
+        "flops_per_launch": st["flops"], "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+        "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+        "kernel": "paged_prefill_mfma_kernel"}
+    del st
+    torch.cuda.empty_cache()
+
+    cache, kc, vc, perm, gen, cases = time_long_decode(torch, args, DEFAULT_LONG_CASES)
+    out["long_decode"] = {
+        "workload": ("split decode, Qwen3-8B heads (32 Q / 8 KV), bf16, pool 65536, hipGraph "
+                     "replay of launches over distinct blocks (plan included)"),
+        "cases": {k: {"us_per_launch": round(us, 2), "gbs": round(b / us / 1e3, 1),
+                      "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+                  for k, (us, b) in cases.items()}}
+    del cache, kc, vc, perm
+    torch.cuda.empty_cache()
+
+    # The reference's CPU-runnable case: fp32, 0.6B shape, pool 1024, 8
+    # sequences with contexts U[64, 512], one append + decode layer call.
+    out["small_fp32_decode"] = small_fp32_decode(torch, args, make_decode_batch, QWEN3_06B,
+                                                 decode_bytes)
+    return out
+
+
+def small_fp32_decode(torch, args, make_decode_batch, shape, decode_bytes) -> dict:
+    from microinfer_amd.layer.hip_paged_attention import hip_paged_decode
+    from microinfer_amd.worker.kv_cache import KVCache
+
+    batch = make_decode_batch(num_seqs=8, ctx_lo=64, ctx_hi=512, pool_blocks=1024, **shape)
+    dev = torch.device("cuda", 0)
+    cache = KVCache(1, 1024, 16, 8, 128, dtype=torch.float32, device=dev, layout=args.layout)
+    cache.keys[0].copy_(torch.from_numpy(batch.key_pool))
+    cache.values[0].copy_(torch.from_numpy(batch.value_pool))
+    q = torch.from_numpy(batch.query).to(dev)
+    nk = torch.from_numpy(batch.new_keys).to(dev)
+    nv = torch.from_numpy(batch.new_values).to(dev)
+    tables = torch.tensor(batch.block_tables, device=dev)
+    lens = torch.tensor(batch.context_lens, device=dev)
+    scale = 1 / math.sqrt(128)
+
+    def call():
+        return hip_paged_decode(q, cache.keys[0], cache.values[0], tables, lens, scale=scale,
+                                new_keys=nk, new_values=nv)
+
+    ms = time_launches(torch, call, args, 50)
+    contexts = [int(c) for c in batch.context_lens]
+    nbytes = decode_bytes(contexts, num_q_heads=16, num_kv_heads=8, head_dim=128, elem_bytes=4,
+                          block_size=16)
+    line = {"workload": ("KV append + paged decode, fp32, Qwen3-0.6B attention (16 Q / 8 KV), "
+                         "block 16, pool 1024, 8 sequences, contexts U[64,512] (seed 0), one "
+                         "layer call (eager, 50 timed)"),
+            "bytes_per_call": nbytes, "us_per_call": round(ms * 1e3, 3),
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2)}
+    if not args.no_cpu_baseline:
+        from oracle import kv_append, paged_attention_reference
+
+        hk, hv = batch.key_pool.copy(), batch.value_pool.copy()
+        slots = np.asarray(batch.slots)
+
+        def one_call():
+            kv_append(hk, hv, slots, batch.new_keys, batch.new_values)
+            return paged_attention_reference(batch.query, hk, hv, batch.block_tables,
+                                             contexts, list(range(9)), scale=scale)
+
+        sec = _median_time(one_call)
+        line["cpu_baseline"] = {
+            "value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": blas_threads(),
+            "kind": "port",
+            "sample": (f"the same layer call (append + decode over {sum(contexts)} tokens) x 5 "
+                       f"after 1 warm-up, median {sec * 1e3:.2f} ms; numpy/BLAS on the host "
+                       f"({cpu_model()})")}
+    log(f"small fp32 decode: {ms * 1e3:.1f} us per call")
+    return line
 
 
 def measure_decode(args) -> dict:
@@ -1484,6 +1615,9 @@ def measure_decode(args) -> dict:
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(DECODE_TRAFFIC),
+            "traffic_source": ("profiles/paged_decode_traffic_qwen3-0.6b_b32.json: rocprofv3 "
+                               "FETCH_SIZE + WRITE_SIZE counter runs of this workload, "
+                               "copy-calibrated; read from the file, not measured in this run"),
             "kernel": "paged_decode_mfma_kernel (fused append + decode + split merge)",
             "bytes_per_launch": layer_bytes,
             "us_per_launch": round(layer_us, 3),
