@@ -268,9 +268,13 @@ def measured_bf16_gemm_peak(torch, n: int = 8192, runs: int = 20) -> dict:
             "us": round(ms * 1e3, 1)}
 
 
+# Launches per prefill step that share one launch plan: Qwen3-8B's 36 layers.
+PREFILL_LAYERS = 36
+
+
 def prefill_state(torch, layout: str) -> dict:
     """The mixed chunked-prefill batch on the device (8B shape, pool 65536)."""
-    from microinfer_amd.layer.hip_paged_attention import hip_paged_prefill
+    from microinfer_amd.layer.hip_paged_attention import hip_paged_prefill, prefill_plan
     from microinfer_amd.workloads import make_mixed_prefill_batch, prefill_flops
     from microinfer_amd.worker.kv_cache import KVCache
 
@@ -290,15 +294,26 @@ def prefill_state(torch, layout: str) -> dict:
     max_q = int(batch.q_lens.max())
     scale = 1 / math.sqrt(128)
 
-    def step():
-        # The output is allocated by the call (from the graph's pool when
-        # captured); the step is the launch alone.
+    def step(planned=True):
+        # One call that plans for itself (planned) or runs unplanned; the
+        # output is allocated by the call (from the graph's pool when
+        # captured).
         return hip_paged_prefill(q, cache.keys[0], cache.values[0], cu_q, cu_k, tables,
-                                 max_seqlen_q=max_q, scale=scale)
+                                 max_seqlen_q=max_q, scale=scale, planned=planned)
+
+    def layers_step():
+        # The engine's pattern: one launch plan per step, shared by the
+        # launches of every layer.
+        plan = prefill_plan(cu_q, cu_k, num_tokens=total_q, num_q_heads=32, num_kv_heads=8,
+                            head_dim=128, dtype=q.dtype, block_size=16,
+                            block_table_width=tables.shape[1])
+        for _ in range(PREFILL_LAYERS):
+            hip_paged_prefill(q, cache.keys[0], cache.values[0], cu_q, cu_k, tables,
+                              max_seqlen_q=max_q, scale=scale, plan=plan)
 
     flops = prefill_flops(batch.q_lens, batch.context_lens, num_q_heads=32, head_dim=128)
-    return dict(batch=batch, cache=cache, q=q, gen=gen, step=step, flops=flops,
-                total_q=total_q, dev=dev)
+    return dict(batch=batch, cache=cache, q=q, gen=gen, step=step, layers_step=layers_step,
+                flops=flops, total_q=total_q, dev=dev)
 
 
 def time_launches(torch, run, args, steps: int) -> float:
@@ -328,17 +343,22 @@ def run_prefill(args) -> int:
     scale = 1 / math.sqrt(128)
     step()
     torch.cuda.synchronize()
-    # A step is one launch: launched eagerly, back to back, the launches queue
-    # behind each other and the events time the kernels; a graph replay per
-    # launch would add its own gap (--graph measures that).
+    # A step is the plan plus one launch per layer (PREFILL_LAYERS), launched
+    # eagerly back to back: the launches queue behind each other and the
+    # events time the kernels; a graph replay would add its own gap (--graph
+    # measures that). The figure is per launch.
     if args.graph:
         graph = torch.cuda.CUDAGraph()
         with capture_graph(graph):
-            step()
+            st["layers_step"]()
         run = graph.replay
     else:
-        run = step
-    ms = time_launches(torch, run, args, args.steps)
+        run = st["layers_step"]
+    ms = time_launches(torch, run, args, max(1, args.steps // 5)) / PREFILL_LAYERS
+    single_ms = time_launches(torch, step, args, args.steps)
+    unplanned_ms = time_launches(torch, lambda: step(planned=False), args, args.steps)
+    log(f"single call (plans for itself): {single_ms * 1e3:.1f} us, unplanned launch: "
+        f"{unplanned_ms * 1e3:.1f} us")
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     if args.copy_calibration_mib:
         copy_calibration(torch, args.copy_calibration_mib)
@@ -353,16 +373,23 @@ def run_prefill(args) -> int:
     dq = torch.randn((d_rows, 32, 128), generator=gen, device=dev).to(torch.bfloat16)
     dk = torch.randn((d_rows, 8, 128), generator=gen, device=dev).to(torch.bfloat16)
     dv = torch.randn((d_rows, 8, 128), generator=gen, device=dev).to(torch.bfloat16)
-    direct = lambda: hip_paged_prefill(dq, dk, dv, d_cu, d_cu, None, max_seqlen_q=512,  # noqa: E731
-                                       scale=scale)
+    from microinfer_amd.layer.hip_paged_attention import prefill_plan
+
+    def direct():
+        plan = prefill_plan(d_cu, d_cu, num_tokens=d_rows, num_q_heads=32, num_kv_heads=8,
+                            head_dim=128, dtype=dq.dtype, num_kv_rows=d_rows, paged=False)
+        for _ in range(PREFILL_LAYERS):
+            hip_paged_prefill(dq, dk, dv, d_cu, d_cu, None, max_seqlen_q=512, scale=scale,
+                              plan=plan)
+
     for _ in range(max(1, args.warmup)):
         direct()
     start.record()
-    for _ in range(args.steps):
+    for _ in range(max(1, args.steps // 5)):
         direct()
     end.record()
     torch.cuda.synchronize()
-    d_ms = start.elapsed_time(end) / args.steps
+    d_ms = start.elapsed_time(end) / max(1, args.steps // 5) / PREFILL_LAYERS
     d_flops = prefill_flops(d_lens, d_lens, num_q_heads=32, head_dim=128)
     log(f"direct prefill: {d_ms * 1e3:.1f} us per launch, {d_flops / d_ms / 1e9:.1f} TFLOP/s")
     result = {
@@ -383,15 +410,23 @@ def run_prefill(args) -> int:
             "workload": ("mixed chunked prefill, Qwen3-8B attention (32 Q / 8 KV heads, "
                          "head_dim 128), bf16, block 16, pool 65536 blocks: 8 chunks of 512 "
                          "rows on prefixes U[0,3072] (first 1024 tokens shared) + 24 decode "
-                         "rows with contexts U[256,2048] (seed 0), one varlen launch per step, "
-                         + ("hipGraph replay" if args.graph else "launched eagerly back to back")),
+                         "rows with contexts U[256,2048] (seed 0); a step is one launch plan "
+                         f"and {PREFILL_LAYERS} varlen launches sharing it (Qwen3-8B's layers), "
+                         + ("hipGraph replay" if args.graph else "launched eagerly back to back")
+                         + "; the figure is per launch"),
             "query_rows": total_q,
+            "launches_per_plan": PREFILL_LAYERS,
+            "single_call_us": round(single_ms * 1e3, 3),
+            "single_call": "one call that plans for itself (plan kernel + launch)",
+            "unplanned_us": round(unplanned_ms * 1e3, 3),
+            "unplanned": "mi_paged_prefill: one workgroup per (query block, KV head), no plan",
             "flops_per_launch": flops,
             "kv_layout": args.layout,
             "direct_prefill_us": round(d_ms * 1e3, 3),
             "direct_prefill_tflops": round(d_flops / d_ms / 1e9, 2),
             "direct_prefill": ("no-prefix prefill of 8 prompts x 512 tokens on contiguous K/V "
-                               "(no block table), same heads, one launch"),
+                               f"(no block table), same heads; one plan per {PREFILL_LAYERS} "
+                               "launches, per launch"),
         },
         "roofline": {
             "bound": "mfma",
@@ -1429,15 +1464,19 @@ def other_workloads(torch, args) -> dict:
     st = prefill_state(torch, args.layout)
     st["step"]()
     torch.cuda.synchronize()
-    ms = time_launches(torch, st["step"], args, 20)
+    ms = time_launches(torch, st["layers_step"], args, 4) / PREFILL_LAYERS
+    single_ms = time_launches(torch, st["step"], args, 20)
     tflops = st["flops"] / (ms * 1e-3) / 1e12
-    log(f"mixed prefill: {ms * 1e3:.1f} us per launch, {tflops:.1f} TFLOP/s")
+    log(f"mixed prefill: {ms * 1e3:.1f} us per launch, {tflops:.1f} TFLOP/s "
+        f"(single self-planning call {single_ms * 1e3:.1f} us)")
     out["prefill"] = {
         "workload": ("mixed chunked prefill, Qwen3-8B attention (32 Q / 8 KV heads), bf16, "
                      "block 16, pool 65536: 8 chunks of 512 rows on prefixes U[0,3072] "
                      "(first 1024 tokens shared) + 24 decode rows, contexts U[256,2048], "
-                     "seed 0; one varlen launch, eager back to back, 20 timed"),
+                     f"seed 0; one launch plan per {PREFILL_LAYERS} varlen launches (eager, "
+                     "back to back, 4 steps timed), per launch"),
         "tflops": round(tflops, 2), "us_per_launch": round(ms * 1e3, 3),
+        "single_call_us": round(single_ms * 1e3, 3),
         "flops_per_launch": st["flops"], "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
         "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
         "kernel": "paged_prefill_mfma_kernel"}

@@ -51,7 +51,8 @@ const char* mi_last_error(void);
 
 /* ABI version of this library (major * 100 + minor). 101: mi_tune_decode and
  * its plan/workspace knobs were removed (workspace and plan sizes depend only
- * on the call's arguments). */
+ * on the call's arguments). 102: mi_paged_prefill_planned,
+ * mi_paged_prefill_plan and mi_paged_prefill_workspace_bytes added. */
 int32_t mi_abi_version(void);
 
 /*
@@ -243,6 +244,70 @@ int32_t mi_paged_prefill(const void* query, int64_t q_token_stride, int64_t q_he
                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                          int32_t block_size, int32_t num_blocks, float scale,
                          int32_t dtype, void* stream);
+
+/*
+ * Workspace for mi_paged_prefill_planned: bytes for num_tokens query rows in
+ * num_requests requests (256-byte aligned, no initialisation needed), or 0
+ * when such a call takes no workspace (then pass NULL): dtype other than
+ * bf16/f16, head_dim other than 128, Hq/Hkv not 1, 2 or 4, more than 4096
+ * requests. The size depends only on these arguments.
+ */
+int64_t mi_paged_prefill_workspace_bytes(int32_t num_tokens, int32_t num_requests,
+                                         int32_t num_q_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, int32_t dtype);
+
+/*
+ * mi_paged_prefill with a launch plan: the same arguments, results within
+ * float rounding of it (partitions merge in a fixed order, so a call's
+ * output does not depend on scheduling), plus a workspace of
+ * mi_paged_prefill_workspace_bytes() (NULL when that is 0).
+ *
+ * A small plan kernel, launched on the same stream ahead of the attention
+ * kernel, splits the key range of (query block, KV head) items with more
+ * key tiles than about 3/4 of a CU's share of the launch into contiguous
+ * partitions (their partials merged by the last one to finish) and orders
+ * the launch largest item first, so one long request's blocks no longer
+ * set the launch time. The reference splits only decode
+ * (microinfer/layer/triton_paged_attention.py:342-349); its prefill grid is
+ * one program per (request, query block, head) (:307-339).
+ * Calls sharing one workspace must be stream-ordered.
+ *
+ * flags: 0, or MI_PREFILL_PLAN_READY when mi_paged_prefill_plan has already
+ * written this call's plan into the workspace (same cu_seqlens contents,
+ * num_tokens, num_requests, heads, paging, block_size, block_table_width and
+ * num_blocks): the plan kernel is then skipped, so one plan serves every
+ * layer of a step.
+ */
+#define MI_PREFILL_PLAN_READY 1
+int32_t mi_paged_prefill_planned(const void* query, int64_t q_token_stride,
+                                 int64_t q_head_stride, const void* key_cache,
+                                 const void* value_cache, int64_t cache_block_stride,
+                                 int64_t cache_token_stride, int64_t cache_head_stride,
+                                 const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                 const int32_t* block_tables, int64_t block_table_stride,
+                                 int32_t block_table_width, void* out,
+                                 int64_t out_token_stride, int64_t out_head_stride,
+                                 int32_t num_tokens, int32_t num_requests,
+                                 int32_t max_seqlen_q, int32_t num_q_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                 int32_t num_blocks, float scale, int32_t dtype,
+                                 void* workspace, int64_t workspace_bytes, int32_t flags,
+                                 void* stream);
+
+/*
+ * The launch plan of mi_paged_prefill_planned alone, written into
+ * `workspace` for later calls with MI_PREFILL_PLAN_READY. paged != 0: the
+ * calls pass block tables of width block_table_width (keys per request are
+ * capped at block_table_width * block_size); paged == 0: contiguous K/V of
+ * num_blocks rows. MI_ERR_UNSUPPORTED when mi_paged_prefill_workspace_bytes
+ * is 0 for these sizes.
+ */
+int32_t mi_paged_prefill_plan(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                              int32_t num_tokens, int32_t num_requests, int32_t num_q_heads,
+                              int32_t num_kv_heads, int32_t head_dim, int32_t paged,
+                              int32_t block_size, int32_t block_table_width,
+                              int32_t num_blocks, int32_t dtype, void* workspace,
+                              int64_t workspace_bytes, void* stream);
 
 /*
  * Block-table gather: copy each request's first c_r cache rows, in logical

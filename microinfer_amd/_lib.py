@@ -66,6 +66,17 @@ SIGNATURES = {
         [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _I32, _P, _I64,
          _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P],
     ),
+    "mi_paged_prefill_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I32, _I32]),
+    "mi_paged_prefill_planned": (
+        _I32,
+        [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _I32, _P, _I64,
+         _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P, _I64, _I32,
+         _P],
+    ),
+    "mi_paged_prefill_plan": (
+        _I32,
+        [_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _I64, _P],
+    ),
     "mi_gather_kv": (
         _I32,
         [_P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P, _I32, _I32, _P, _P, _I32, _I32,

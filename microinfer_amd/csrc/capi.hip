@@ -28,4 +28,4 @@ int32_t check_launch(const char* what) {
 
 extern "C" const char* mi_last_error(void) { return mi::g_last_error.c_str(); }
 
-extern "C" int32_t mi_abi_version(void) { return 101; }
+extern "C" int32_t mi_abi_version(void) { return 102; }

@@ -12,6 +12,14 @@ struct alignas(32) PlanItem {
   int32_t seq, blk_begin, blk_end, nparts, first_item, ctx, part, unused;
 };
 
+// One prefill work item: query row block `qblock` (rows qblock * BM ..) of
+// request `req`, key tiles [tile_begin, tile_end). A (row block, KV head)
+// whose keys are split runs as `nparts` items, partition `part` publishing
+// its partial in slot `slot + part` and arriving at counter `counter`.
+struct alignas(32) PrefillItem {
+  int32_t req, qblock, tile_begin, tile_end, part, nparts, slot, counter;
+};
+
 // Arguments of the vector (non-MFMA) paged attention kernels. Strides are in
 // elements; head_dim is contiguous everywhere.
 struct AttnArgs {
@@ -32,6 +40,12 @@ struct AttnArgs {
   float* ws_ml;   // split partials: [items, Hkv, G, 2] (log2-domain max, sum)
   int32_t* counters;  // [num_seqs * Hkv] arrival counts; zero on entry and exit
   const PlanItem* plan;  // decode: [max_items] work items
+  // MFMA prefill with a plan (optional): [max_entries] items, the first
+  // *prefill_count of them used; partials in ws_acc / ws_ml, arrivals in
+  // counters.
+  const PrefillItem* prefill_plan;
+  const int32_t* prefill_count;
+  int32_t max_entries;
   // Decode with fused append (optional): row s of new_k/new_v is written to
   // position ctx_s - 1 of sequence s and attended to from registers.
   const void* new_k;
@@ -56,6 +70,18 @@ int32_t launch_paged_attention_vector(const AttnArgs& args, int32_t dtype,
 // this call, and its launch.
 bool prefill_mfma_supported(const AttnArgs& args, int32_t dtype);
 int32_t launch_prefill_mfma(const AttnArgs& args, int32_t dtype, hipStream_t stream);
+// Workspace of a planned MFMA prefill launch (0: the call cannot be planned),
+// and the planned launch itself: the plan kernel, then the attention kernel.
+// `workspace` is 256-byte aligned and at least prefill_workspace_bytes()
+// long; it needs no initialisation.
+int64_t prefill_workspace_bytes(int32_t num_rows, int32_t num_seqs, int32_t group,
+                                int32_t num_kv_heads);
+int32_t prefill_counters(int32_t num_kv_heads);
+// The plan kernel alone (its result serves every planned launch with the
+// same cu_seqlens and sizes until they change).
+int32_t launch_prefill_plan(const AttnArgs& args, void* workspace, hipStream_t stream);
+int32_t launch_prefill_mfma_planned(AttnArgs args, int32_t dtype, void* workspace,
+                                    bool plan_ready, hipStream_t stream);
 
 // MFMA decode kernel (paged_decode_mfma.hip): 16-bit caches, head_dim 128,
 // up to 16 query heads per KV head, block size >= 16, paged.

@@ -233,30 +233,33 @@ extern "C" int32_t mi_paged_decode_append(
                           stream);
 }
 
-extern "C" int32_t mi_paged_prefill(
-    const void* query, int64_t q_token_stride, int64_t q_head_stride, const void* key_cache,
-    const void* value_cache, int64_t cache_block_stride, int64_t cache_token_stride,
-    int64_t cache_head_stride, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-    const int32_t* block_tables, int64_t block_table_stride, int32_t block_table_width,
-    void* out, int64_t out_token_stride, int64_t out_head_stride, int32_t num_tokens,
-    int32_t num_requests, int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads,
-    int32_t head_dim, int32_t block_size, int32_t num_blocks, float scale, int32_t dtype,
-    void* stream) {
+namespace {
+int32_t paged_prefill(
+    const char* name, const void* query, int64_t q_token_stride, int64_t q_head_stride,
+    const void* key_cache, const void* value_cache, int64_t cache_block_stride,
+    int64_t cache_token_stride, int64_t cache_head_stride, const int32_t* cu_seqlens_q,
+    const int32_t* cu_seqlens_k, const int32_t* block_tables, int64_t block_table_stride,
+    int32_t block_table_width, void* out, int64_t out_token_stride, int64_t out_head_stride,
+    int32_t num_tokens, int32_t num_requests, int32_t max_seqlen_q, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t num_blocks, float scale,
+    int32_t dtype, void* workspace, int64_t workspace_bytes, int32_t flags, void* stream) {
   using namespace mi;
   clear_error();
-  int32_t st = check_common("mi_paged_prefill", dtype, num_q_heads, num_kv_heads, head_dim,
+  const std::string fn(name);
+  if (flags & ~MI_PREFILL_PLAN_READY) return fail(MI_ERR_INVALID_ARGUMENT, fn + ": unknown flags");
+  int32_t st = check_common(name, dtype, num_q_heads, num_kv_heads, head_dim,
                             block_size, num_blocks, block_table_width);
   if (st != MI_OK) return st;
   if (num_tokens < 0 || num_requests < 0 || max_seqlen_q < 0)
-    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_prefill: negative sizes");
+    return fail(MI_ERR_INVALID_ARGUMENT, fn + ": negative sizes");
   if (num_tokens == 0) return MI_OK;
   if (num_requests == 0)
-    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_prefill: tokens without requests");
+    return fail(MI_ERR_INVALID_ARGUMENT, fn + ": tokens without requests");
   if (max_seqlen_q == 0)
-    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_prefill: max_seqlen_q must be positive");
+    return fail(MI_ERR_INVALID_ARGUMENT, fn + ": max_seqlen_q must be positive");
   // block_tables may be NULL: contiguous varlen K/V (see mi_attn.h).
   if (!query || !key_cache || !value_cache || !cu_seqlens_q || !cu_seqlens_k || !out)
-    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_prefill: null pointer");
+    return fail(MI_ERR_INVALID_ARGUMENT, fn + ": null pointer");
   const int64_t es = static_cast<int64_t>(dtype_size(dtype));
   const int64_t vec = std::min<int64_t>(head_dim, 16 / es);
   const int64_t vb = vec * es;
@@ -264,7 +267,7 @@ extern "C" int32_t mi_paged_prefill(
       !aligned(out, vb) || q_token_stride % vec || q_head_stride % vec ||
       cache_block_stride % vec || cache_token_stride % vec || cache_head_stride % vec ||
       out_token_stride % vec || out_head_stride % vec)
-    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_prefill: misaligned pointers or strides");
+    return fail(MI_ERR_INVALID_ARGUMENT, fn + ": misaligned pointers or strides");
 
   AttnArgs a{};
   a.q = query;
@@ -294,9 +297,102 @@ extern "C" int32_t mi_paged_prefill(
   a.num_blocks = num_blocks;
   a.scale_log2 = scale * kLog2e;
   a.varlen = 1;
-  // bf16/f16 with head_dim 128 and GQA groups 1, 2, 4 run on MFMA; every
-  // other supported shape on the vector kernel.
-  if (prefill_mfma_supported(a, dtype))
-    return launch_prefill_mfma(a, dtype, static_cast<hipStream_t>(stream));
-  return dispatch_vector(a, dtype, static_cast<hipStream_t>(stream));
+  // bf16/f16 with head_dim 128 and GQA groups 1, 2, 4 run on MFMA (planned
+  // when a workspace is given); every other supported shape on the vector
+  // kernel.
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (prefill_mfma_supported(a, dtype)) {
+    if (workspace == nullptr) return launch_prefill_mfma(a, dtype, s);
+    const int64_t need = prefill_workspace_bytes(num_tokens, num_requests, a.group, num_kv_heads);
+    if (need == 0) return launch_prefill_mfma(a, dtype, s);  // too many requests to plan
+    if (workspace_bytes < need || !aligned(workspace, 256))
+      return fail(MI_ERR_WORKSPACE, fn + ": workspace needs " + std::to_string(need) +
+                                        " bytes, 256-byte aligned");
+    return launch_prefill_mfma_planned(a, dtype, workspace, (flags & MI_PREFILL_PLAN_READY) != 0,
+                                       s);
+  }
+  return dispatch_vector(a, dtype, s);
+}
+}  // namespace
+
+extern "C" int32_t mi_paged_prefill(
+    const void* query, int64_t q_token_stride, int64_t q_head_stride, const void* key_cache,
+    const void* value_cache, int64_t cache_block_stride, int64_t cache_token_stride,
+    int64_t cache_head_stride, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+    const int32_t* block_tables, int64_t block_table_stride, int32_t block_table_width,
+    void* out, int64_t out_token_stride, int64_t out_head_stride, int32_t num_tokens,
+    int32_t num_requests, int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int32_t num_blocks, float scale, int32_t dtype,
+    void* stream) {
+  return paged_prefill("mi_paged_prefill", query, q_token_stride, q_head_stride, key_cache,
+                       value_cache, cache_block_stride, cache_token_stride, cache_head_stride,
+                       cu_seqlens_q, cu_seqlens_k, block_tables, block_table_stride,
+                       block_table_width, out, out_token_stride, out_head_stride, num_tokens,
+                       num_requests, max_seqlen_q, num_q_heads, num_kv_heads, head_dim,
+                       block_size, num_blocks, scale, dtype, nullptr, 0, 0, stream);
+}
+
+extern "C" int64_t mi_paged_prefill_workspace_bytes(int32_t num_tokens, int32_t num_requests,
+                                                    int32_t num_q_heads, int32_t num_kv_heads,
+                                                    int32_t head_dim, int32_t dtype) {
+  if ((dtype != MI_DTYPE_BF16 && dtype != MI_DTYPE_F16) || head_dim != 128 ||
+      num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
+    return 0;
+  return mi::prefill_workspace_bytes(num_tokens, num_requests, num_q_heads / num_kv_heads,
+                                     num_kv_heads);
+}
+
+extern "C" int32_t mi_paged_prefill_planned(
+    const void* query, int64_t q_token_stride, int64_t q_head_stride, const void* key_cache,
+    const void* value_cache, int64_t cache_block_stride, int64_t cache_token_stride,
+    int64_t cache_head_stride, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+    const int32_t* block_tables, int64_t block_table_stride, int32_t block_table_width,
+    void* out, int64_t out_token_stride, int64_t out_head_stride, int32_t num_tokens,
+    int32_t num_requests, int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int32_t num_blocks, float scale, int32_t dtype,
+    void* workspace, int64_t workspace_bytes, int32_t flags, void* stream) {
+  return paged_prefill("mi_paged_prefill_planned", query, q_token_stride, q_head_stride,
+                       key_cache, value_cache, cache_block_stride, cache_token_stride,
+                       cache_head_stride, cu_seqlens_q, cu_seqlens_k, block_tables,
+                       block_table_stride, block_table_width, out, out_token_stride,
+                       out_head_stride, num_tokens, num_requests, max_seqlen_q, num_q_heads,
+                       num_kv_heads, head_dim, block_size, num_blocks, scale, dtype, workspace,
+                       workspace_bytes, flags, stream);
+}
+
+extern "C" int32_t mi_paged_prefill_plan(const int32_t* cu_seqlens_q,
+                                         const int32_t* cu_seqlens_k, int32_t num_tokens,
+                                         int32_t num_requests, int32_t num_q_heads,
+                                         int32_t num_kv_heads, int32_t head_dim, int32_t paged,
+                                         int32_t block_size, int32_t block_table_width,
+                                         int32_t num_blocks, int32_t dtype, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+  using namespace mi;
+  clear_error();
+  const int64_t need = mi_paged_prefill_workspace_bytes(num_tokens, num_requests, num_q_heads,
+                                                        num_kv_heads, head_dim, dtype);
+  if (need == 0)
+    return fail(MI_ERR_UNSUPPORTED, "mi_paged_prefill_plan: these sizes take no plan");
+  if (!cu_seqlens_q || !cu_seqlens_k)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_prefill_plan: null pointer");
+  if (paged && (!is_pow2(block_size) || block_table_width < 0))
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_prefill_plan: invalid block size or width");
+  if (!paged && num_blocks < 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_prefill_plan: negative K/V rows");
+  if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 256))
+    return fail(MI_ERR_WORKSPACE, "mi_paged_prefill_plan: workspace needs " +
+                                      std::to_string(need) + " bytes, 256-byte aligned");
+  AttnArgs a{};
+  a.cu_q = cu_seqlens_q;
+  a.cu_k = cu_seqlens_k;
+  // Only the null-ness of the tables matters to the plan.
+  a.tables = paged ? cu_seqlens_q : nullptr;
+  a.t_width = block_table_width;
+  a.block_size = paged ? block_size : 1;
+  a.num_blocks = num_blocks;
+  a.num_seqs = num_requests;
+  a.num_rows = num_tokens;
+  a.num_kv_heads = num_kv_heads;
+  a.group = num_q_heads / num_kv_heads;
+  return launch_prefill_plan(a, workspace, static_cast<hipStream_t>(stream));
 }

@@ -24,6 +24,8 @@ capture); the library never allocates.
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import math
 
 import torch
@@ -68,6 +70,9 @@ def _check_caches(key_cache: torch.Tensor, value_cache: torch.Tensor):
 # still point at it.
 _counters: dict[tuple[int, int], torch.Tensor] = {}
 _retired_counters: list[torch.Tensor] = []
+
+
+_PLAN_READY = 1  # MI_PREFILL_PLAN_READY
 
 
 def _decode_counters(device: torch.device, stream: int, needed: int) -> torch.Tensor:
@@ -230,6 +235,55 @@ def hip_paged_decode(
     return output
 
 
+@dataclass(frozen=True)
+class PrefillPlan:
+    """Launch plan of planned prefill calls (``prefill_plan``): the workspace
+    it was written into and the call sizes it was made for."""
+
+    workspace: torch.Tensor
+    key: tuple
+
+
+def _prefill_key(num_tokens, num_requests, num_q_heads, num_kv_heads, head_dim, dtype, paged,
+                 block_size, block_table_width, num_blocks) -> tuple:
+    return (num_tokens, num_requests, num_q_heads, num_kv_heads, head_dim, dtype, bool(paged),
+            block_size if paged else 0, block_table_width if paged else 0,
+            0 if paged else num_blocks)
+
+
+def prefill_plan(cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, *, num_tokens: int,
+                 num_q_heads: int, num_kv_heads: int, head_dim: int, dtype: torch.dtype,
+                 block_size: int = 0, block_table_width: int = 0,
+                 num_kv_rows: int = 0, paged: bool = True) -> PrefillPlan | None:
+    """Launch plan for the prefill calls of one step (shared by every layer).
+
+    Computed on the device from the cu_seqlens (so a hipGraph can hold it);
+    pass it to ``hip_paged_prefill(..., plan=...)`` for calls with these sizes
+    (paged: block tables of width ``block_table_width``; contiguous K/V:
+    ``num_kv_rows`` rows). None when these sizes run unplanned.
+    """
+    _lib.require_device(cu_seqlens_q, cu_seqlens_k, what="prefill_plan")
+    cu_seqlens_q = _index32(cu_seqlens_q)
+    cu_seqlens_k = _index32(cu_seqlens_k)
+    num_requests = cu_seqlens_q.numel() - 1
+    lib = _lib.load()
+    code = _lib.dtype_code(dtype)
+    nbytes = lib.mi_paged_prefill_workspace_bytes(num_tokens, num_requests, num_q_heads,
+                                                  num_kv_heads, head_dim, code)
+    if nbytes <= 0:
+        return None
+    workspace = torch.empty(nbytes, dtype=torch.uint8, device=cu_seqlens_q.device)
+    status = lib.mi_paged_prefill_plan(
+        cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), num_tokens, num_requests, num_q_heads,
+        num_kv_heads, head_dim, int(paged), block_size, block_table_width, num_kv_rows, code,
+        workspace.data_ptr(), nbytes, _lib.stream_handle(cu_seqlens_q.device),
+    )
+    _lib.check(status, "mi_paged_prefill_plan")
+    key = _prefill_key(num_tokens, num_requests, num_q_heads, num_kv_heads, head_dim, code,
+                       paged, block_size, block_table_width, num_kv_rows)
+    return PrefillPlan(workspace, key)
+
+
 def hip_paged_prefill(
     query: torch.Tensor,
     key_cache: torch.Tensor,
@@ -240,6 +294,8 @@ def hip_paged_prefill(
     *,
     max_seqlen_q: int,
     scale: float | None = None,
+    planned: bool = True,
+    plan: PrefillPlan | None = None,
 ) -> torch.Tensor:
     """Causal varlen attention straight from the paged cache (bottom-right mask).
 
@@ -248,6 +304,13 @@ def hip_paged_prefill(
     which the caller appended first). With ``block_tables=None`` the "caches"
     are contiguous ``[sum c, Hkv, D]`` K/V and request r's keys start at row
     ``cu_seqlens_k[r]``.
+
+    ``planned`` (default) runs the MFMA kernel behind its launch plan
+    (``mi_paged_prefill_planned``: long items split along their keys, largest
+    first); False runs ``mi_paged_prefill``, one workgroup per (query block,
+    KV head) and no workspace. Both agree to float rounding. ``plan``: a
+    ``prefill_plan(...)`` result for this call's cu_seqlens and sizes, which
+    skips the plan kernel (one plan per step serves every layer).
     """
     if query.ndim != 3:
         raise ValueError("query must have shape [tokens, Hq, D]")
@@ -307,16 +370,37 @@ def hip_paged_prefill(
     if scale is None:
         scale = 1.0 / math.sqrt(head_dim)
 
-    status = _lib.load().mi_paged_prefill(
+    lib = _lib.load()
+    dtype = _lib.dtype_code(query.dtype)
+    flags = 0
+    if plan is not None:
+        if not planned:
+            raise ValueError("a plan needs planned=True")
+        key = _prefill_key(num_tokens, num_requests, num_q_heads, num_kv_heads, head_dim, dtype,
+                           paged, block_size, t_width, num_blocks)
+        if not isinstance(plan, PrefillPlan) or plan.key != key:
+            raise ValueError("plan must come from prefill_plan() with this call's sizes")
+        _lib.require_device(plan.workspace, what="hip_paged_prefill")
+        workspace, ws_bytes, flags = plan.workspace, plan.workspace.numel(), _PLAN_READY
+    else:
+        # The launch plan's workspace (split partials, the plan, its
+        # counters): from the caching allocator, so a captured graph owns it.
+        ws_bytes = (lib.mi_paged_prefill_workspace_bytes(num_tokens, num_requests, num_q_heads,
+                                                         num_kv_heads, head_dim, dtype)
+                    if planned else 0)
+        workspace = (torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
+                     if ws_bytes > 0 else None)
+    status = lib.mi_paged_prefill_planned(
         query.data_ptr(), query.stride(0), query.stride(1),
         key_cache.data_ptr(), value_cache.data_ptr(), c_bs, c_ts, c_hs,
         cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), t_ptr, t_stride, t_width,
         output.data_ptr(), output.stride(0), output.stride(1),
         num_tokens, num_requests, int(max_seqlen_q), num_q_heads, num_kv_heads, head_dim,
-        block_size, num_blocks, float(scale), _lib.dtype_code(query.dtype),
+        block_size, num_blocks, float(scale), dtype,
+        workspace.data_ptr() if workspace is not None else None, ws_bytes, flags,
         _lib.stream_handle(query.device),
     )
-    _lib.check(status, "mi_paged_prefill")
+    _lib.check(status, "mi_paged_prefill_planned")
     return output
 
 

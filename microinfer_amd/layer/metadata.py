@@ -37,6 +37,7 @@ class AttentionMetadata:
     _slot_blocks: torch.Tensor | None = field(default=None, repr=False)
     _slot_offsets: torch.Tensor | None = field(default=None, repr=False)
     _decode_plans: dict = field(default_factory=dict, repr=False)
+    _prefill_plans: dict = field(default_factory=dict, repr=False)
 
     @classmethod
     def build(
@@ -104,6 +105,32 @@ class AttentionMetadata:
                                block_size=block_size, block_table_width=key[2])
             self._decode_plans[key] = plan
         return plan
+
+    def prefill_plan(self, query: torch.Tensor, key_cache: torch.Tensor, *, paged: bool = True):
+        """Device launch plan for this step's prefill calls, built once and
+        reused by every layer (None where such calls run unplanned)."""
+        if self.cu_seqlens_q is None or not self.cu_seqlens_q.is_cuda:
+            return None
+        from microinfer_amd.layer.hip_paged_attention import prefill_plan
+
+        num_tokens, num_q_heads, head_dim = query.shape
+        if paged:
+            if self.block_tables is None:
+                return None
+            _, block_size, num_kv_heads, _ = key_cache.shape
+            width, rows = self.block_tables.shape[1], 0
+        else:
+            block_size, width = 0, 0
+            rows, num_kv_heads = max(key_cache.shape[0], 1), key_cache.shape[1]
+        key = (num_tokens, num_q_heads, num_kv_heads, head_dim, query.dtype, paged, block_size,
+               width, rows)
+        if key not in self._prefill_plans:
+            cu_k = self.cu_seqlens_k if self.cu_seqlens_k is not None else self.cu_seqlens_q
+            self._prefill_plans[key] = prefill_plan(
+                self.cu_seqlens_q, cu_k, num_tokens=num_tokens, num_q_heads=num_q_heads,
+                num_kv_heads=num_kv_heads, head_dim=head_dim, dtype=query.dtype,
+                block_size=block_size, block_table_width=width, num_kv_rows=rows, paged=paged)
+        return self._prefill_plans[key]
 
     @property
     def cu_q_cpu(self) -> tuple[int, ...]:

@@ -105,6 +105,7 @@ def paged_attention_meta(
         metadata.block_tables,
         max_seqlen_q=max_q,
         scale=scale,
+        plan=metadata.prefill_plan(query, key_cache),
     )
 
 
@@ -128,5 +129,6 @@ def varlen_attention(query, keys, values, metadata: AttentionMetadata, *, scale=
     if max_q <= 0:
         max_q = max(metadata.q_lens_cpu, default=0)
     return hip_paged_prefill(
-        query, keys, values, cu_q, cu_k, None, max_seqlen_q=max_q, scale=scale
+        query, keys, values, cu_q, cu_k, None, max_seqlen_q=max_q, scale=scale,
+        plan=metadata.prefill_plan(query, keys, paged=False),
     )

@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_clean_error_state():
     lib = _lib.load()
-    assert lib.mi_abi_version() == 101
+    assert lib.mi_abi_version() == 102
     assert isinstance(_lib.last_error(), str)
 
 
@@ -107,6 +107,38 @@ def test_workspace_size_formula(split_k):
     items = plan // 32
     partials = 0 if split_k == 1 else items * 8 * 4 * (128 + 2) * 4
     assert size == plan_region + partials
+
+
+def test_prefill_workspace_size_and_refusal():
+    lib = _lib.load()
+    r256 = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    # bf16, 4120 rows in 32 requests, 32 Q / 8 KV heads: 1024 partial slots
+    # (128 partitions x 8 KV heads) of 4 wave regions, 64 counters per KV head.
+    regions = 128 * 8 * 4
+    entries = (4120 + 31) // 32 + 32 + 128
+    need = lib.mi_paged_prefill_workspace_bytes(4120, 32, 32, 8, 128, 2)
+    assert need == (256 + r256(64 * 8 * 4) + r256(entries * 32) + r256(regions * 2 * 64 * 4)
+                    + regions * 4096 * 4)
+    assert lib.mi_paged_prefill_workspace_bytes(4120, 32, 32, 8, 128, 1) == need  # f16
+    # No workspace where the call is not planned.
+    assert lib.mi_paged_prefill_workspace_bytes(4120, 32, 32, 8, 128, 0) == 0  # f32
+    assert lib.mi_paged_prefill_workspace_bytes(4120, 32, 32, 8, 64, 2) == 0
+    assert lib.mi_paged_prefill_workspace_bytes(4120, 32, 64, 8, 128, 2) == 0  # group 8
+    assert lib.mi_paged_prefill_workspace_bytes(8192, 4097, 32, 8, 128, 2) == 0
+    fake = ctypes.c_void_p(256)
+    args = [fake, 4096, 128, fake, fake, 16384, 1024, 128, fake, fake, fake, 256, 256,
+            fake, 4096, 128, 4120, 32, 512, 32, 8, 128, 16, 65536, 0.088, 2]
+    assert lib.mi_paged_prefill_planned(*args, fake, need - 1, 0, None) == 3
+    assert "workspace" in _lib.last_error()
+    misaligned = ctypes.c_void_p(256 + 16)
+    assert lib.mi_paged_prefill_planned(*args, misaligned, need, 0, None) == 3
+    assert lib.mi_paged_prefill_planned(*args, fake, need, 2, None) == 1  # unknown flag
+    # The plan alone: the same sizes and workspace rules.
+    plan_args = [fake, fake, 4120, 32, 32, 8, 128, 1, 16, 256, 65536, 2]
+    assert lib.mi_paged_prefill_plan(*plan_args, fake, need - 1, None) == 3
+    assert lib.mi_paged_prefill_plan(*plan_args[:-1], 0, fake, need, None) == 2  # f32
+    bad_block = plan_args[:8] + [12] + plan_args[9:]
+    assert lib.mi_paged_prefill_plan(*bad_block, fake, need, None) == 1
 
 
 def test_dense_ops_validate_before_launch():

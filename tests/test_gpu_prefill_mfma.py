@@ -83,8 +83,9 @@ def test_group_sizes_and_tile_edges(hq, hkv, dtype):
 
 @pytest.mark.parametrize("block_size", [16, 32, 64, 128, 256])
 def test_block_sizes(block_size):
-    q_lens = [5, 64, 100]
-    prefixes = [block_size - 3, 2 * block_size + 1, 0]
+    # The single row's context spans several blocks and ends mid-tile.
+    q_lens = [5, 64, 100, 1]
+    prefixes = [block_size - 3, 2 * block_size + 1, 0, 3 * block_size + 20]
     q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, 32, 8, block_size,
                                                           torch.bfloat16, 2)
     out = _run(q, kc, vc, tables, cu_q, cu_k)
@@ -132,6 +133,7 @@ def test_nan_in_unused_slots_and_invalid_blocks_stays_out():
     assert not torch.isfinite(vc[0]).any()
     bad = tables.clone()
     bad[1, 2] = -1
+    bad[2, 5] = -1  # a single-row request
     bad[3, 0] = 10 ** 6
     out = _run(q, kc, vc, bad, cu_q, cu_k)
     assert torch.isfinite(out).all()
@@ -140,20 +142,22 @@ def test_nan_in_unused_slots_and_invalid_blocks_stays_out():
 def test_invalid_table_entries_are_masked():
     # A -1 and an out-of-range id inside the contexts: those blocks drop out
     # of the softmax (as in the decode kernel) and are never dereferenced.
-    q_lens = [40, 20]
-    prefixes = [60, 10]
+    q_lens = [40, 20, 1]
+    prefixes = [60, 10, 90]
     q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, 16, 8, 16,
                                                           torch.bfloat16, 4)
     bad = tables.clone()
     bad[0, 1] = -1
     bad[1, 0] = 10 ** 6
+    bad[2, 0] = -1  # the single row's first tile
+    bad[2, 3] = 10 ** 6
     out = _run(q, kc, vc, bad, cu_q, cu_k)
     assert torch.isfinite(out).all()
     # Expected: the same attention with those blocks' keys excluded.
     host_t = bad.cpu().numpy()
     ref = np.zeros(as_f32(out).shape, dtype=np.float64)
     kf, vf, qf = as_f32(kc), as_f32(vc), as_f32(q)
-    for r in range(2):
+    for r in range(3):
         c, ql = contexts[r], q_lens[r]
         pos = np.arange(c)
         blk = host_t[r, pos // 16]
@@ -190,6 +194,67 @@ def test_contiguous_kv_matches_dense(dtype):
         for a, b in zip(cu[:-1], cu[1:])
     ])
     assert max_abs(out, expected) <= 2e-2
+
+
+@pytest.mark.parametrize("hq", [8, 16, 32])
+def test_single_rows_over_long_contexts(hq):
+    # Single-row requests (the decode rows of a mixed step) take a path of
+    # their own: 16-position tiles spread over the workgroup's four waves.
+    # Contexts around multiples of 16 and 64 and up to 2 K positions.
+    q_lens = [1] * 7 + [48]
+    prefixes = [0, 15, 16, 63, 64, 1023, 2047, 200]
+    q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, hq, 8, 16,
+                                                          torch.bfloat16, 6)
+    out = _run(q, kc, vc, tables, cu_q, cu_k)
+    expected = oracle_prefill(q, kc, vc, tables, contexts, cu_q, 1 / math.sqrt(D))
+    assert max_abs(out, expected) <= 2e-2
+
+
+def test_planned_launch_splits_merge_deterministically():
+    # Long prefixes make the plan split (query block, KV head) items along
+    # their keys (target 8-13 tiles here); the merged result must match the
+    # unsplit launch to float rounding, the oracle to the usual bound, and
+    # be the same bits on every call whatever order the partitions finish in.
+    q_lens = [512, 96, 1, 200, 1, 33]
+    prefixes = [2500, 1300, 3000, 0, 17, 700]
+    for hq in (32, 16, 8):
+        q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, hq, 8, 16,
+                                                              torch.bfloat16, 8)
+        args = (q, kc, vc, torch.tensor(cu_q, device=DEV), torch.tensor(cu_k, device=DEV),
+                tables)
+        kw = dict(max_seqlen_q=max(q_lens), scale=1 / math.sqrt(D))
+        first = hip_paged_prefill(*args, **kw)
+        for _ in range(3):
+            assert torch.equal(hip_paged_prefill(*args, **kw), first)
+        unplanned = hip_paged_prefill(*args, planned=False, **kw)
+        assert max_abs(first, as_f32(unplanned)) <= 1e-2
+        expected = oracle_prefill(q, kc, vc, tables, contexts, cu_q, 1 / math.sqrt(D))
+        assert max_abs(first, expected) <= 2e-2
+        assert max_abs(unplanned, expected) <= 2e-2
+
+
+def test_one_plan_serves_many_calls():
+    # A plan made once (per step) and passed to several calls gives the bits
+    # of a call that plans for itself; a plan for other sizes is refused.
+    from microinfer_amd.layer.hip_paged_attention import prefill_plan
+
+    q_lens = [300, 1, 64, 1]
+    prefixes = [2000, 900, 40, 5]
+    q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, 32, 8, 16,
+                                                          torch.bfloat16, 9)
+    cq, ck = torch.tensor(cu_q, device=DEV), torch.tensor(cu_k, device=DEV)
+    kw = dict(max_seqlen_q=max(q_lens), scale=1 / math.sqrt(D))
+    own = hip_paged_prefill(q, kc, vc, cq, ck, tables, **kw)
+    plan = prefill_plan(cq, ck, num_tokens=q.shape[0], num_q_heads=32, num_kv_heads=8,
+                        head_dim=D, dtype=q.dtype, block_size=16,
+                        block_table_width=tables.shape[1])
+    assert plan is not None
+    for _ in range(3):
+        assert torch.equal(hip_paged_prefill(q, kc, vc, cq, ck, tables, plan=plan, **kw), own)
+    with pytest.raises(ValueError, match="prefill_plan"):
+        hip_paged_prefill(q[:-1], kc, vc, cq, ck, tables, plan=plan, **kw)
+    expected = oracle_prefill(q, kc, vc, tables, contexts, cu_q, 1 / math.sqrt(D))
+    assert max_abs(own, expected) <= 2e-2
 
 
 def test_long_prefix_chunk():
