@@ -355,10 +355,12 @@ def run_prefill(args) -> int:
     else:
         run = st["layers_step"]
     ms = time_launches(torch, run, args, max(1, args.steps // 5)) / PREFILL_LAYERS
-    single_ms = time_launches(torch, step, args, args.steps)
-    unplanned_ms = time_launches(torch, lambda: step(planned=False), args, args.steps)
-    log(f"single call (plans for itself): {single_ms * 1e3:.1f} us, unplanned launch: "
-        f"{unplanned_ms * 1e3:.1f} us")
+    single_ms = unplanned_ms = None
+    if not args.planned_only:
+        single_ms = time_launches(torch, step, args, args.steps)
+        unplanned_ms = time_launches(torch, lambda: step(planned=False), args, args.steps)
+        log(f"single call (plans for itself): {single_ms * 1e3:.1f} us, unplanned launch: "
+            f"{unplanned_ms * 1e3:.1f} us")
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     if args.copy_calibration_mib:
         copy_calibration(torch, args.copy_calibration_mib)
@@ -416,9 +418,9 @@ def run_prefill(args) -> int:
                          + "; the figure is per launch"),
             "query_rows": total_q,
             "launches_per_plan": PREFILL_LAYERS,
-            "single_call_us": round(single_ms * 1e3, 3),
+            "single_call_us": round(single_ms * 1e3, 3) if single_ms else None,
             "single_call": "one call that plans for itself (plan kernel + launch)",
-            "unplanned_us": round(unplanned_ms * 1e3, 3),
+            "unplanned_us": round(unplanned_ms * 1e3, 3) if unplanned_ms else None,
             "unplanned": "mi_paged_prefill: one workgroup per (query block, KV head), no plan",
             "flops_per_launch": flops,
             "kv_layout": args.layout,
@@ -1377,6 +1379,10 @@ def main() -> int:
     parser.add_argument("--layout", default="paired",
                         choices=["paired", "head_major", "token_major"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--planned-only", action="store_true",
+                        help="prefill: time only the launches that share one plan per step "
+                             "(no self-planning or unplanned calls of the same kernel), e.g. "
+                             "for kernel profiling")
     parser.add_argument("--no-engine", action="store_true",
                         help="decode: leave out the engine half of the line (decode tok/s of "
                              "the Qwen3-0.6B engine workload), e.g. for kernel profiling")
