@@ -288,3 +288,123 @@ def test_pool_beyond_int32_offsets_matches_small_pool():
     assert torch.equal(small, big)
     expected = oracle_prefill(q, kc, vc, tables, contexts, cu_q, 1 / math.sqrt(D))
     assert max_abs(big, expected) <= 2e-2
+
+
+def _read_plan(plan, num_tokens, num_requests, hq, hkv):
+    """Items of a prefill plan, read back from its workspace (the layout
+    mi_paged_prefill_workspace_bytes sizes: count, counters, items)."""
+    r256 = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    part_cap = max(2, 1024 // hkv)
+    counters = part_cap // 2 * hkv
+    bm = 128 // (hq // hkv)
+    max_entries = (num_tokens + bm - 1) // bm + num_requests + part_cap
+    raw = plan.workspace.cpu()
+    count = int(raw[:4].view(torch.int32)[0])
+    assert 0 < count <= max_entries
+    off = 256 + r256(counters * 4)
+    items = raw[off:off + count * 32].view(torch.int32).reshape(count, 8).numpy()
+    return items, part_cap, counters
+
+
+def test_plan_items_cover_every_block_once_largest_first():
+    # Few items on long contexts: the plan splits; every (request, row block)
+    # must appear with key ranges that partition its tiles, each split with
+    # its own partial slots and counter, listed by size, largest first.
+    from microinfer_amd.layer.hip_paged_attention import prefill_plan
+
+    q_lens = [64, 1, 40, 1]
+    prefixes = [6000, 3000, 500, 20]
+    hq, hkv = 32, 8
+    _, _, _, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, hq, hkv, 16,
+                                                        torch.bfloat16, 10)
+    total = sum(q_lens)
+    plan = prefill_plan(torch.tensor(cu_q, device=DEV), torch.tensor(cu_k, device=DEV),
+                        num_tokens=total, num_q_heads=hq, num_kv_heads=hkv, head_dim=D,
+                        dtype=torch.bfloat16, block_size=16, block_table_width=tables.shape[1])
+    items, part_cap, counters = _read_plan(plan, total, len(q_lens), hq, hkv)
+    bm = 32
+    expected = {}
+    for r, (ql, c) in enumerate(zip(q_lens, contexts)):
+        for b in range((ql + bm - 1) // bm):
+            kv_end = min(c, c - ql + min(ql, (b + 1) * bm))
+            expected[(r, b)] = (kv_end + 31) // 32
+    seen = {}
+    slots, ctrs, sizes = set(), set(), []
+    for req, qb, t0, t1, part, nparts, slot, ctr in items.tolist():
+        assert (req, qb) in expected
+        seen.setdefault((req, qb), []).append((part, nparts, t0, t1, slot, ctr))
+        single = q_lens[req] == 1
+        sizes.append(-(-contexts[req] // 96) if single else t1 - t0)
+        if nparts > 1:
+            assert not single
+            assert slot + part < part_cap
+            assert ctr * hkv < counters
+            slots.add(slot + part)
+            ctrs.add(ctr)
+    assert set(seen) == set(expected)
+    split = 0
+    for key, parts in seen.items():
+        n = parts[0][1]
+        assert sorted(p[0] for p in parts) == list(range(n))
+        assert all(p[1] == n for p in parts)
+        if n > 1:
+            split += 1
+            assert len({(p[4], p[5]) for p in parts}) == 1  # one slot base, one counter
+        ranges = sorted((p[2], p[3]) for p in parts)
+        assert ranges[0][0] == 0 and ranges[-1][1] == expected[key]
+        assert all(a[1] == b[0] for a, b in zip(ranges, ranges[1:]))
+        assert all(t1 > t0 for t0, t1 in ranges)
+    assert split > 0  # the long request's blocks were split
+    assert len(ctrs) == split
+    assert sizes == sorted(sizes, reverse=True)
+
+
+@pytest.mark.parametrize("hq,dtype", [(8, torch.bfloat16), (16, torch.bfloat16),
+                                      (32, torch.float16)])
+def test_split_launches_match_oracle_across_groups_and_dtypes(hq, dtype):
+    # Few long items make the plan split; groups 1 and 2 have 128- and
+    # 64-row blocks, f16 its own conversions.
+    q_lens = [96, 1, 200]
+    prefixes = [5000, 2000, 3000]
+    q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, hq, 8, 16, dtype,
+                                                          11)
+    args = (q, kc, vc, torch.tensor(cu_q, device=DEV), torch.tensor(cu_k, device=DEV), tables)
+    kw = dict(max_seqlen_q=max(q_lens), scale=1 / math.sqrt(D))
+    planned = hip_paged_prefill(*args, **kw)
+    unplanned = hip_paged_prefill(*args, planned=False, **kw)
+    assert max_abs(planned, as_f32(unplanned)) <= 1e-2
+    expected = oracle_prefill(q, kc, vc, tables, contexts, cu_q, 1 / math.sqrt(D))
+    assert max_abs(planned, expected) <= 2e-2
+
+
+def _causal_f64(q, k, v, scale):
+    """Causal GQA attention of one no-prefix prompt in float64 (numpy)."""
+    q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
+    rows, hq, _ = q.shape
+    group = hq // k.shape[1]
+    out = np.empty_like(q)
+    mask = np.tril(np.ones((rows, rows), dtype=bool))
+    for h in range(hq):
+        s = (q[:, h] @ k[:, h // group].T) * scale
+        s = np.where(mask, s, -np.inf)
+        w = np.exp(s - s.max(axis=1, keepdims=True))
+        out[:, h] = (w / w.sum(axis=1, keepdims=True)) @ v[:, h // group]
+    return out
+
+
+def test_contiguous_kv_split_matches_dense():
+    # One long no-prefix prompt on one KV head: 32 row blocks, so the plan
+    # splits the later blocks' keys on the contiguous path too.
+    gen = torch.Generator().manual_seed(12)
+    rows = 1024
+    q = torch.randn(rows, 4, D, generator=gen).to(torch.bfloat16).to(DEV)
+    k = torch.randn(rows, 1, D, generator=gen).to(torch.bfloat16).to(DEV)
+    v = torch.randn(rows, 1, D, generator=gen).to(torch.bfloat16).to(DEV)
+    cu = torch.tensor([0, rows], dtype=torch.int32, device=DEV)
+    kw = dict(max_seqlen_q=rows, scale=1 / math.sqrt(D))
+    planned = hip_paged_prefill(q, k, v, cu, cu, None, **kw)
+    assert torch.equal(hip_paged_prefill(q, k, v, cu, cu, None, **kw), planned)
+    unplanned = hip_paged_prefill(q, k, v, cu, cu, None, planned=False, **kw)
+    assert max_abs(planned, as_f32(unplanned)) <= 1e-2
+    expected = _causal_f64(as_f32(q), as_f32(k), as_f32(v), 1 / math.sqrt(D))
+    assert max_abs(planned, expected) <= 2e-2
