@@ -295,7 +295,8 @@ def prefill_state(torch, layout: str) -> dict:
     scale = 1 / math.sqrt(128)
 
     def step(planned=True):
-        # One call that plans for itself (planned) or runs unplanned; the
+        # One call without a shared plan (it plans for itself only when
+        # short of items) or, planned=False, always unplanned; the
         # output is allocated by the call (from the graph's pool when
         # captured).
         return hip_paged_prefill(q, cache.keys[0], cache.values[0], cu_q, cu_k, tables,
@@ -359,7 +360,7 @@ def run_prefill(args) -> int:
     if not args.planned_only:
         single_ms = time_launches(torch, step, args, args.steps)
         unplanned_ms = time_launches(torch, lambda: step(planned=False), args, args.steps)
-        log(f"single call (plans for itself): {single_ms * 1e3:.1f} us, unplanned launch: "
+        log(f"single call (no shared plan): {single_ms * 1e3:.1f} us, unplanned launch: "
             f"{unplanned_ms * 1e3:.1f} us")
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     if args.copy_calibration_mib:
@@ -419,7 +420,9 @@ def run_prefill(args) -> int:
             "query_rows": total_q,
             "launches_per_plan": PREFILL_LAYERS,
             "single_call_us": round(single_ms * 1e3, 3) if single_ms else None,
-            "single_call": "one call that plans for itself (plan kernel + launch)",
+            "single_call": ("one call without a shared plan: it plans for itself only when it "
+                            "has fewer (query block, KV head) items than two per CU (this "
+                            "batch has more, so it runs unplanned)"),
             "unplanned_us": round(unplanned_ms * 1e3, 3) if unplanned_ms else None,
             "unplanned": "mi_paged_prefill: one workgroup per (query block, KV head), no plan",
             "flops_per_launch": flops,
@@ -1474,7 +1477,7 @@ def other_workloads(torch, args) -> dict:
     single_ms = time_launches(torch, st["step"], args, 20)
     tflops = st["flops"] / (ms * 1e-3) / 1e12
     log(f"mixed prefill: {ms * 1e3:.1f} us per launch, {tflops:.1f} TFLOP/s "
-        f"(single self-planning call {single_ms * 1e3:.1f} us)")
+        f"(single call without a shared plan {single_ms * 1e3:.1f} us)")
     out["prefill"] = {
         "workload": ("mixed chunked prefill, Qwen3-8B attention (32 Q / 8 KV heads), bf16, "
                      "block 16, pool 65536: 8 chunks of 512 rows on prefixes U[0,3072] "

@@ -73,6 +73,14 @@ _retired_counters: list[torch.Tensor] = []
 
 
 _PLAN_READY = 1  # MI_PREFILL_PLAN_READY
+_cus: dict[int, int] = {}
+
+
+def _device_cus(device: torch.device) -> int:
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if index not in _cus:
+        _cus[index] = torch.cuda.get_device_properties(index).multi_processor_count
+    return _cus[index]
 
 
 def _decode_counters(device: torch.device, stream: int, needed: int) -> torch.Tensor:
@@ -305,12 +313,14 @@ def hip_paged_prefill(
     are contiguous ``[sum c, Hkv, D]`` K/V and request r's keys start at row
     ``cu_seqlens_k[r]``.
 
-    ``planned`` (default) runs the MFMA kernel behind its launch plan
+    ``planned`` (default) runs the MFMA kernel behind a launch plan
     (``mi_paged_prefill_planned``: long items split along their keys, largest
-    first); False runs ``mi_paged_prefill``, one workgroup per (query block,
-    KV head) and no workspace. Both agree to float rounding. ``plan``: a
-    ``prefill_plan(...)`` result for this call's cu_seqlens and sizes, which
-    skips the plan kernel (one plan per step serves every layer).
+    first) when the call has fewer (query block, KV head) items than two per
+    CU, else unplanned; False always runs ``mi_paged_prefill``, one
+    workgroup per (query block, KV head) and no workspace. Both agree to
+    float rounding. ``plan``: a ``prefill_plan(...)`` result for this call's
+    cu_seqlens and sizes, which skips the plan kernel (one plan per step
+    serves every layer) and is always used.
     """
     if query.ndim != 3:
         raise ValueError("query must have shape [tokens, Hq, D]")
@@ -383,6 +393,16 @@ def hip_paged_prefill(
         _lib.require_device(plan.workspace, what="hip_paged_prefill")
         workspace, ws_bytes, flags = plan.workspace, plan.workspace.numel(), _PLAN_READY
     else:
+        # A call that plans for itself pays the plan kernel (≈ 7 µs): worth
+        # it only where the launch is short of items to keep two workgroups
+        # on every CU (there the plan splits long items: one 8192-token
+        # request 207 → 64 µs); with more items the unplanned order is
+        # within a few per cent. A plan shared by a step's layers
+        # (``plan=``) always pays off.
+        if planned:
+            rows_per_block = 128 * num_kv_heads // num_q_heads if num_q_heads else 128
+            items = (num_tokens // max(rows_per_block, 1) + num_requests) * num_kv_heads
+            planned = items < 2 * _device_cus(query.device)
         # The launch plan's workspace (split partials, the plan, its
         # counters): from the caching allocator, so a captured graph owns it.
         ws_bytes = (lib.mi_paged_prefill_workspace_bytes(num_tokens, num_requests, num_q_heads,

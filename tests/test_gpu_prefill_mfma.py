@@ -408,3 +408,17 @@ def test_contiguous_kv_split_matches_dense():
     assert max_abs(planned, as_f32(unplanned)) <= 1e-2
     expected = _causal_f64(as_f32(q), as_f32(k), as_f32(v), 1 / math.sqrt(D))
     assert max_abs(planned, expected) <= 2e-2
+
+
+def test_call_with_many_items_runs_unplanned():
+    # 8 x 512 rows with 8 KV heads: 1088 (query block, KV head) items, more
+    # than two per CU, so a call without a shared plan skips the plan kernel
+    # and its output is the unplanned launch's, bit for bit.
+    q_lens = [512] * 8
+    prefixes = [0, 16, 100, 300, 40, 7, 512, 1]
+    q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, 32, 8, 16,
+                                                          torch.bfloat16, 13)
+    args = (q, kc, vc, torch.tensor(cu_q, device=DEV), torch.tensor(cu_k, device=DEV), tables)
+    kw = dict(max_seqlen_q=512, scale=1 / math.sqrt(D))
+    assert torch.equal(hip_paged_prefill(*args, **kw),
+                       hip_paged_prefill(*args, planned=False, **kw))
