@@ -422,3 +422,43 @@ def test_call_with_many_items_runs_unplanned():
     kw = dict(max_seqlen_q=512, scale=1 / math.sqrt(D))
     assert torch.equal(hip_paged_prefill(*args, **kw),
                        hip_paged_prefill(*args, planned=False, **kw))
+
+
+@pytest.mark.parametrize("block_size", [32, 64, 256])
+def test_split_launches_across_block_sizes(block_size):
+    # Long contexts on few items (so the plan splits) with tiles spanning
+    # part of a block or several blocks.
+    q_lens = [70, 1, 33]
+    prefixes = [4000 + block_size // 2, 2500, 3000 - 5]
+    q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, 32, 8, block_size,
+                                                          torch.bfloat16, 14)
+    args = (q, kc, vc, torch.tensor(cu_q, device=DEV), torch.tensor(cu_k, device=DEV), tables)
+    kw = dict(max_seqlen_q=max(q_lens), scale=1 / math.sqrt(D))
+    planned = hip_paged_prefill(*args, **kw)
+    assert max_abs(planned, as_f32(hip_paged_prefill(*args, planned=False, **kw))) <= 1e-2
+    expected = oracle_prefill(q, kc, vc, tables, contexts, cu_q, 1 / math.sqrt(D))
+    assert max_abs(planned, expected) <= 2e-2
+
+
+def test_split_launch_with_nan_pool_and_invalid_ids_stays_finite():
+    # Split items whose ranges cross invalid table entries, over a pool whose
+    # unused slots hold NaN: every partition masks what it cannot see, the
+    # merge weighs empty partitions zero, and the result equals the unsplit
+    # launch's to float rounding.
+    q_lens = [64, 1, 40]
+    prefixes = [3500, 2000, 2600]
+    q, kc, vc, tables, contexts, cu_q, cu_k = _paged_case(q_lens, prefixes, 32, 8, 16,
+                                                          torch.bfloat16, 15,
+                                                          poison=float("nan"))
+    bad = tables.clone()
+    bad[0, 5] = -1
+    bad[0, 150] = 10 ** 6
+    bad[1, 70] = -1
+    bad[2, 0] = -1
+    args = (q, kc, vc, torch.tensor(cu_q, device=DEV), torch.tensor(cu_k, device=DEV), bad)
+    kw = dict(max_seqlen_q=max(q_lens), scale=1 / math.sqrt(D))
+    planned = hip_paged_prefill(*args, **kw)
+    assert torch.isfinite(planned).all()
+    unplanned = hip_paged_prefill(*args, planned=False, **kw)
+    assert torch.isfinite(unplanned).all()
+    assert max_abs(planned, as_f32(unplanned)) <= 1e-2
