@@ -18,8 +18,8 @@
 // [j*VEC, (j+1)*VEC) of the first half and the same of the second half
 // (split-half pairs (i, i + D/2)), or 2*VEC consecutive elements (interleaved
 // pairs (2i, 2i + 1)), so every rotation pair sits in one lane, and the mean
-// square is a reduction over the group (DPP). A wave handles 64 / L rows at
-// once; the grid covers the flat (token, row) space.
+// square is a reduction over the group (DPP). A wave handles one token: its
+// 64 / L groups take the token's rows in turn.
 #include "mi_common.h"
 
 namespace mi {
@@ -32,6 +32,12 @@ __device__ __forceinline__ float round_to(float x) {
   return E::load(E::store(x));
 }
 
+// A token per `wpt` waves: the token's position, slot and angles are read
+// once per wave (each lane keeps the cos/sin of its pairs), then the waves'
+// 64 / L lane groups take the token's rows in turn (group g of wave w:
+// rows g + (64 / L) (w + wpt i)), two rows' loads in flight per group. Large
+// launches use one wave per token (the angles read once per token); small
+// ones spread a token over as many waves as it has row groups.
 template <typename E, bool INTERLEAVED, int L>
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(
     const typename E::raw* __restrict__ qkv, int64_t qkv_ts,
@@ -42,20 +48,22 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(
     typename E::raw* __restrict__ k_out, int64_t ko_ts, int64_t ko_hs,
     typename E::raw* __restrict__ kc, typename E::raw* __restrict__ vc, int64_t c_bs,
     int64_t c_ts, int64_t c_hs, int hq, int hkv, int num_tokens, int block_size,
-    int num_blocks) {
+    int num_blocks, int wpt) {
   using R = typename E::raw;
   constexpr int VEC = 16 / sizeof(R);
   constexpr int HALF = L * VEC;  // D / 2
   constexpr int D = 2 * HALF;
+  constexpr int GROUPS = kWave / L;
   using V = Pack<R, VEC>;
+  const int lane = threadIdx.x % kWave;
+  const int64_t gw = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) +
+                    static_cast<int>(threadIdx.x) / kWave;
+  const int t = static_cast<int>(gw / wpt);
+  const int w = static_cast<int>(gw % wpt);
+  if (t >= num_tokens) return;  // the whole wave
+  const int g = lane / L;  // lane group: one row at a time
+  const int j = lane % L;  // lane within the group
   const int rows_per_token = hq + 2 * hkv;
-  const int64_t row = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) / L;
-  const int j = threadIdx.x % L;  // lane within the row's group
-  // Groups past the last row still take part in the shuffles below with
-  // their own (unused) values; they only skip memory.
-  const bool live = row < static_cast<int64_t>(num_tokens) * rows_per_token;
-  const int t = live ? static_cast<int>(row / rows_per_token) : 0;
-  const int r = live ? static_cast<int>(row % rows_per_token) : 0;
 
   const int64_t pos = pos64 ? static_cast<const int64_t*>(positions)[t]
                             : static_cast<const int32_t*>(positions)[t];
@@ -63,40 +71,18 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(
   // zeros to q_out / k_out and nothing is appended.
   const bool pos_ok = pos >= 0 && pos < table_len;
   int64_t dst = -1;  // element offset of the token's cache row (head 0)
-  if (slots != nullptr && pos_ok && live) {
+  if (slots != nullptr && pos_ok) {
     const int32_t slot = slots[t];
     if (slot >= 0) {
       const int32_t blk = slot / block_size;
       if (blk < num_blocks) dst = blk * c_bs + (slot - blk * block_size) * c_ts;
     }
   }
-  const R* src = qkv + t * qkv_ts + static_cast<int64_t>(r) * D;
-  // Element offsets of this lane's two vectors within the row.
+  // Element offsets of this lane's two vectors within a row: split-half
+  // pairs (i, i + D/2) or interleaved pairs (2i, 2i + 1), so every rotation
+  // pair sits in one lane (pair k of the lane has angle index j*VEC + k).
   const int oa = INTERLEAVED ? 2 * j * VEC : j * VEC;
   const int ob = INTERLEAVED ? 2 * j * VEC + VEC : HALF + j * VEC;
-
-  if (r >= hq + hkv) {  // value row: appended as projected
-    if (live && dst >= 0) {
-      const int h = r - hq - hkv;
-      store_pack<R, VEC>(vc + dst + h * c_hs + oa, load_pack<R, VEC>(src + oa));
-      store_pack<R, VEC>(vc + dst + h * c_hs + ob, load_pack<R, VEC>(src + ob));
-    }
-    return;
-  }
-  const bool is_q = r < hq;
-  const int h = is_q ? r : r - hq;
-  // Every load of the row is issued before any arithmetic: the row, the norm
-  // weights and the position's angles (pair k of this lane has angle index
-  // j*VEC + k in both layouts).
-  V va = zero_pack<R, VEC>(), vb = zero_pack<R, VEC>();
-  if (live) {
-    va = load_pack<R, VEC>(src + oa);
-    vb = load_pack<R, VEC>(src + ob);
-  }
-  const R* w = is_q ? q_weight : k_weight;
-  const V wa = load_pack<R, VEC>(w + oa), wb = load_pack<R, VEC>(w + ob);
-  // The angles as 16-byte vectors (the tables are 16-byte aligned and a
-  // lane's VEC angles start at a multiple of 4 floats).
   static_assert(VEC % 4 == 0, "angles load as whole float4 vectors");
   const float* crow = cos_t + (pos_ok ? pos : 0) * HALF + j * VEC;
   const float* srow = sin_t + (pos_ok ? pos : 0) * HALF + j * VEC;
@@ -111,67 +97,100 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(
       sn[k + i] = pos_ok ? s4.v[i] : 0.f;
     }
   }
-  // Pair k of this lane: (x[k], y[k]) = (first, second) element of the pair.
-  float x[VEC], y[VEC];
-  float ss = 0.f;
+  const V qwa = load_pack<R, VEC>(q_weight + oa), qwb = load_pack<R, VEC>(q_weight + ob);
+  const V kwa = load_pack<R, VEC>(k_weight + oa), kwb = load_pack<R, VEC>(k_weight + ob);
+  const R* src_t = qkv + t * qkv_ts;
+
+  // Norm, rotation and stores of row r (vectors va, vb already loaded).
+  auto finish_row = [&](int r, const V& va, const V& vb) __attribute__((always_inline)) {
+    if (r >= hq + hkv) {  // value row: appended as projected
+      if (dst >= 0) {
+        const int h = r - hq - hkv;
+        store_pack<R, VEC>(vc + dst + h * c_hs + oa, va);
+        store_pack<R, VEC>(vc + dst + h * c_hs + ob, vb);
+      }
+      return;
+    }
+    const bool is_q = r < hq;
+    const int h = is_q ? r : r - hq;
+    float x[VEC], y[VEC];
+    float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < VEC; ++k) {
-    if constexpr (INTERLEAVED) {
-      // Vector a holds pairs 0 .. VEC/2 - 1, vector b the rest.
-      const V& src_v = k < VEC / 2 ? va : vb;
-      const int e = 2 * (k % (VEC / 2));
-      x[k] = E::load(src_v.v[e]);
-      y[k] = E::load(src_v.v[e + 1]);
-    } else {
-      x[k] = E::load(va.v[k]);
-      y[k] = E::load(vb.v[k]);
+    for (int k = 0; k < VEC; ++k) {
+      if constexpr (INTERLEAVED) {
+        // Vector a holds pairs 0 .. VEC/2 - 1, vector b the rest.
+        const V& src_v = k < VEC / 2 ? va : vb;
+        const int e = 2 * (k % (VEC / 2));
+        x[k] = E::load(src_v.v[e]);
+        y[k] = E::load(src_v.v[e + 1]);
+      } else {
+        x[k] = E::load(va.v[k]);
+        y[k] = E::load(vb.v[k]);
+      }
+      ss = fmaf(x[k], x[k], fmaf(y[k], y[k], ss));
     }
-    ss = fmaf(x[k], x[k], fmaf(y[k], y[k], ss));
-  }
-  ss = group_sum<L>(ss);
-  if (!live) return;
-  const float inv = 1.f / sqrtf(ss / static_cast<float>(D) + eps);
-  V outa, outb;
+    ss = group_sum<L>(ss);
+    const float inv = 1.f / sqrtf(ss / static_cast<float>(D) + eps);
+    const V& wa = is_q ? qwa : kwa;
+    const V& wb = is_q ? qwb : kwb;
+    V outa, outb;
 #pragma unroll
-  for (int k = 0; k < VEC; ++k) {
-    float wx, wy;
-    if constexpr (INTERLEAVED) {
-      const V& wv = k < VEC / 2 ? wa : wb;
-      const int e = 2 * (k % (VEC / 2));
-      wx = E::load(wv.v[e]);
-      wy = E::load(wv.v[e + 1]);
-    } else {
-      wx = E::load(wa.v[k]);
-      wy = E::load(wb.v[k]);
+    for (int k = 0; k < VEC; ++k) {
+      float wx, wy;
+      if constexpr (INTERLEAVED) {
+        const V& wv = k < VEC / 2 ? wa : wb;
+        const int e = 2 * (k % (VEC / 2));
+        wx = E::load(wv.v[e]);
+        wy = E::load(wv.v[e + 1]);
+      } else {
+        wx = E::load(wa.v[k]);
+        wy = E::load(wb.v[k]);
+      }
+      const float nx = round_to<E>(x[k] * inv * wx);
+      const float ny = round_to<E>(y[k] * inv * wy);
+      const R rx = E::store(nx * cs[k] - ny * sn[k]);
+      const R ry = E::store(ny * cs[k] + nx * sn[k]);
+      if constexpr (INTERLEAVED) {
+        V& ov = k < VEC / 2 ? outa : outb;
+        const int e = 2 * (k % (VEC / 2));
+        ov.v[e] = rx;
+        ov.v[e + 1] = ry;
+      } else {
+        outa.v[k] = rx;
+        outb.v[k] = ry;
+      }
     }
-    const float nx = round_to<E>(x[k] * inv * wx);
-    const float ny = round_to<E>(y[k] * inv * wy);
-    const R rx = E::store(nx * cs[k] - ny * sn[k]);
-    const R ry = E::store(ny * cs[k] + nx * sn[k]);
-    if constexpr (INTERLEAVED) {
-      V& ov = k < VEC / 2 ? outa : outb;
-      const int e = 2 * (k % (VEC / 2));
-      ov.v[e] = rx;
-      ov.v[e + 1] = ry;
-    } else {
-      outa.v[k] = rx;
-      outb.v[k] = ry;
-    }
-  }
-  if (is_q) {
-    R* o = q_out + t * qo_ts + h * qo_hs;
-    store_pack<R, VEC>(o + oa, outa);
-    store_pack<R, VEC>(o + ob, outb);
-  } else {
-    if (k_out != nullptr) {
-      R* o = k_out + t * ko_ts + h * ko_hs;
+    if (is_q) {
+      R* o = q_out + t * qo_ts + h * qo_hs;
       store_pack<R, VEC>(o + oa, outa);
       store_pack<R, VEC>(o + ob, outb);
+    } else {
+      if (k_out != nullptr) {
+        R* o = k_out + t * ko_ts + h * ko_hs;
+        store_pack<R, VEC>(o + oa, outa);
+        store_pack<R, VEC>(o + ob, outb);
+      }
+      if (dst >= 0) {
+        store_pack<R, VEC>(kc + dst + h * c_hs + oa, outa);
+        store_pack<R, VEC>(kc + dst + h * c_hs + ob, outb);
+      }
     }
-    if (dst >= 0) {
-      store_pack<R, VEC>(kc + dst + h * c_hs + oa, outa);
-      store_pack<R, VEC>(kc + dst + h * c_hs + ob, outb);
+  };
+  // Rows g, g + GROUPS, ...: two rows' loads issued before either is used.
+  // A group's condition is uniform over its L lanes, as the norm's
+  // reduction needs.
+  const int step = GROUPS * wpt;
+  for (int r0 = g + GROUPS * w; r0 < rows_per_token; r0 += 2 * step) {
+    const int r1 = r0 + step;
+    const V a0 = load_pack<R, VEC>(src_t + r0 * D + oa);
+    const V b0 = load_pack<R, VEC>(src_t + r0 * D + ob);
+    V a1 = zero_pack<R, VEC>(), b1 = zero_pack<R, VEC>();
+    if (r1 < rows_per_token) {
+      a1 = load_pack<R, VEC>(src_t + r1 * D + oa);
+      b1 = load_pack<R, VEC>(src_t + r1 * D + ob);
     }
+    finish_row(r0, a0, b0);
+    if (r1 < rows_per_token) finish_row(r1, a1, b1);
   }
 }
 
@@ -186,8 +205,14 @@ int32_t launch_typed(bool interleaved, const void* qkv, int64_t qkv_ts, const vo
   using R = typename E::raw;
   constexpr int VEC = 16 / sizeof(R);
   const int lanes = d / (2 * VEC);
-  const int64_t rows = static_cast<int64_t>(tokens) * (hq + 2 * hkv);
-  const int64_t grid = (rows * lanes + kThreads - 1) / kThreads;
+  constexpr int kWavesPerBlock = kThreads / kWave;
+  // Waves per token: one when the launch has tokens enough to fill the
+  // chip, else one per row group of the token.
+  const int rows_per_token = hq + 2 * hkv;
+  const int groups = kWave / lanes;
+  const int wpt = tokens >= 4 * device_cus() ? 1 : (rows_per_token + groups - 1) / groups;
+  const int64_t grid =
+      (static_cast<int64_t>(tokens) * wpt + kWavesPerBlock - 1) / kWavesPerBlock;
   if (grid > INT32_MAX) return fail(MI_ERR_UNSUPPORTED, "mi_qk_norm_rope_append: too many rows");
   bool launched = false;
   auto go = [&](auto kernel) {
@@ -196,7 +221,7 @@ int32_t launch_typed(bool interleaved, const void* qkv, int64_t qkv_ts, const vo
         static_cast<const R*>(kw), eps, cos_t, sin_t, table_len, positions, pos64, slots,
         static_cast<R*>(q_out), qo_ts, qo_hs, static_cast<R*>(k_out), ko_ts, ko_hs,
         static_cast<R*>(kc), static_cast<R*>(vc), c_bs, c_ts, c_hs, hq, hkv, tokens,
-        block_size, num_blocks);
+        block_size, num_blocks, wpt);
     launched = true;
   };
 #define MI_QKNR_L(LN)                                                         \
