@@ -39,7 +39,9 @@ __global__ __launch_bounds__(256) void gather_kv_kernel(
   const int64_t wb = static_cast<int64_t>(word) * sizeof(W);
   const int64_t out = (static_cast<int64_t>(row) * num_heads + head) * words_per_row * sizeof(W) + wb;
   W kval{}, vval{};
-  if (logical_block < t_width) {
+  // pos < 0 only for a malformed cu_seqlens_k (first entry above zero):
+  // such rows read as zeros, like rows of invalid blocks.
+  if (pos >= 0 && logical_block < t_width) {
     const int blk = tables[lo * t_stride + logical_block];
     if (blk >= 0 && blk < num_blocks) {
       const int64_t src = blk * c_bs + (pos & (block_size - 1)) * c_ts + head * c_hs + wb;
@@ -81,7 +83,7 @@ __global__ __launch_bounds__(256) void gather_kv_row_kernel(
   const int pos = row - cuk[req];
   const int logical_block = pos >> log2_block;
   int64_t base = -1;
-  if (logical_block < t_width) {
+  if (pos >= 0 && logical_block < t_width) {
     const int blk = ((const ConstI32*)(tables))[req * t_stride + logical_block];
     if (blk >= 0 && blk < num_blocks) base = blk * c_bs + (pos & (block_size - 1)) * c_ts;
   }
