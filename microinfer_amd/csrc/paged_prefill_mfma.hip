@@ -967,7 +967,10 @@ int64_t max_cache_offset(const AttnArgs& a) {
 //    (at least kMinPartTiles, at most kMaxParts ranges), raised until the
 //    ranges fit the workspace's partial slots. A launch with plenty of
 //    items (T above its largest item) is not split at all.
-// Single-row requests (never split) count ctx / kSingleRowDiv tiles.
+// Single-row requests (never split) count ctx / kSingleRowDiv tiles: a
+// single-row workgroup streams its context latency-bound, so it is placed
+// as if it had more tiles than its work alone would say (the mixed 4120-row
+// step: 111.1 us at 48, 113.3 at 96, 112.4 at 40; A/B on two boxes).
 // ---------------------------------------------------------------------------
 constexpr int kPlanThreads = 256;
 constexpr int kPlanPer = 16;  // row blocks per plan thread (registers)
@@ -976,7 +979,7 @@ constexpr int kMaxPlanReqs = 2048;
 constexpr int kPlanBuckets = 2 * kPlanThreads;  // sizes >= 511 share the first
 constexpr int kMinPartTiles = 16;
 constexpr int kSplitSlots = 1024;  // partial slots (partition x KV head)
-constexpr int kSingleRowDiv = 96;
+constexpr int kSingleRowDiv = 48;
 constexpr int64_t kPlanHeader = 256;  // [0]: number of items
 
 // Exclusive scan of one value per thread over the workgroup (wave scans on
